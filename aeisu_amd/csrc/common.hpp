@@ -1,0 +1,119 @@
+// Shared device helpers for the gfx950 (CDNA4) AEISU kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * Activations live in HBM as NHWC tiles: skip/work = FP16 [B][Hq][Wq][32],
+//    low = FP16/E4M3/INT8 [B][Hl][Wl][64], meta = FP16 [B][Hq][Wq][64].
+//  * MFMA 16x16 tiles: operand lane l holds row/column (l & 15) and the
+//    K-slots 8*(l>>4)..+7 (f16 / fp8 K=32) or 16*(l>>4)..+15 (i8 K=64);
+//    the accumulator lane l holds column (l & 15), rows 4*(l>>4)+r, r=0..3.
+//    Weight matrices are pre-permuted on the host so that each lane's
+//    K-slots map to contiguous activation channels.
+//  * Kernels are persistent over tiles: blocks walk tiles with a stride of
+//    gridDim.x, so weights are staged into registers once per wave.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace aeisu {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int i4 __attribute__((ext_vector_type(4)));
+typedef int i8v __attribute__((ext_vector_type(8)));
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+
+constexpr float kE4M3Max = 448.0f;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ f4 mfma_f16(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma_fp8(long a, long b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ i4 mfma_i8(i4 a, i4 b, i4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Cross-row lane exchanges of CDNA4 (v_permlane32_swap: lanes 32-63 of x <-> lanes 0-31 of y;
+// v_permlane16_swap: odd 16-lane rows of x <-> even rows of y).  Written as inline asm on
+// purpose: with the ROCm 7.2 compiler, adding the two results of the
+// __builtin_amdgcn_permlane{16,32}_swap builtin is miscompiled into r[0] + r[0].
+__device__ __forceinline__ void permlane32_swap(float& x, float& y) {
+  asm volatile("v_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ void permlane16_swap(float& x, float& y) {
+  asm volatile("v_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+}
+
+// LeakyReLU as written by the reference epilogues: negative inputs scaled by the slope.
+__device__ __forceinline__ float leaky(float v, float slope) { return v < 0.0f ? v * slope : v; }
+
+// float -> OCP E4M3 with round-to-nearest-even and saturation to +-448.
+// The hardware convert rounds to nearest even but yields NaN above the
+// saturation threshold, so the value is clamped first.
+__device__ __forceinline__ unsigned pack_e4m3x2(float a, float b) {
+  a = __builtin_amdgcn_fmed3f(a, -kE4M3Max, kE4M3Max);
+  b = __builtin_amdgcn_fmed3f(b, -kE4M3Max, kE4M3Max);
+  return (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+__device__ __forceinline__ unsigned pack_e4m3x4(float a, float b, float c, float d) {
+  return pack_e4m3x2(a, b) | (pack_e4m3x2(c, d) << 16);
+}
+// E4M3 byte SEL of word w -> float (exact).
+template <int SEL>
+__device__ __forceinline__ float e4m3_to_f32(unsigned w) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)w, SEL);
+}
+
+// Symmetric INT8: clamp(rint(v * inv), -127, 127)  (rint = round half to even).
+__device__ __forceinline__ int quant_s8(float v, float inv) {
+  float q = __builtin_rintf(v * inv);
+  q = __builtin_amdgcn_fmed3f(q, -127.0f, 127.0f);
+  return (int)q;
+}
+__device__ __forceinline__ unsigned pack_s8x4(int a, int b, int c, int d) {
+  return (unsigned)(a & 255) | ((unsigned)(b & 255) << 8) | ((unsigned)(c & 255) << 16) |
+         ((unsigned)(d & 255) << 24);
+}
+
+__device__ __forceinline__ unsigned short f2h_bits(float v) {
+  _Float16 h = (_Float16)v;
+  return __builtin_bit_cast(unsigned short, h);
+}
+__device__ __forceinline__ unsigned pack_h2(float a, float b) {
+  return (unsigned)f2h_bits(a) | ((unsigned)f2h_bits(b) << 16);
+}
+__device__ __forceinline__ float h2f_lo(unsigned w) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float h2f_hi(unsigned w) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+}
+
+// Tile scheduler: the i-th tile handled by this block.  Blocks are spread
+// round-robin over the 8 XCDs; tiles are assigned so that consecutive tiles
+// (which share halos) run on the same XCD and hit the same L2.
+__device__ __forceinline__ int tile_of(int iter, int num_tiles) {
+  const int grid = (int)gridDim.x;
+  const int b = (int)blockIdx.x;
+  if (grid % 8 != 0) return b + iter * grid;
+  const int per_xcd = grid / 8;
+  const int xcd = b % 8, local = b / 8;
+  const int band = (num_tiles + 7) / 8;              // tiles owned by one XCD
+  const int t = xcd * band + local + iter * per_xcd;
+  return (t < (xcd + 1) * band) ? t : num_tiles;      // past the band -> no tile
+}
+__device__ __forceinline__ int tile_iters(int num_tiles) {
+  const int grid = (int)gridDim.x;
+  if (grid % 8 != 0) return (num_tiles + grid - 1) / grid;
+  const int band = (num_tiles + 7) / 8;
+  return (band + grid / 8 - 1) / (grid / 8);
+}
+
+}  // namespace aeisu

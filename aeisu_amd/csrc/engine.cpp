@@ -1,0 +1,882 @@
+// AEISU runtime engine for MI355X: artifact validation, weight-fragment packing,
+// scratch allocation, the per-frame launch sequence, HIP graphs and stage timing.
+//
+// Reference counterparts: ModelArtifact::Load (optimized/native/src/neural/srcpyr/
+// SrcPyrModel.cpp:243-470), SharedExecutionEngine::UploadModel / AttachConfiguration /
+// EnqueueGraphBody (SrcPyrCudaRuntime.cu:2924-3170, 3310-3806, 4131-4873).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "aeisu_amd.h"
+#include "kernels.hpp"
+#include "sha256.hpp"
+
+namespace aeisu {
+
+// ------------------------------------------------------------------------------------------------
+// errors
+// ------------------------------------------------------------------------------------------------
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+[[noreturn]] static void fail(int code, const std::string& msg) { throw Error(code, msg); }
+static void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(AEISU_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// ------------------------------------------------------------------------------------------------
+// SPYR8F8 artifact (layout: SrcPyrModel.cpp:37-81)
+// ------------------------------------------------------------------------------------------------
+constexpr size_t kHeaderSize = 512, kDescSize = 80, kChecksumOffset = 184, kAlign = 64;
+constexpr const char* kArchitecture = "aif16x5_learnedrgb4dir8_s32_parallel32x4_learnedbase_oc25_v1";
+enum DType : uint32_t { kE4M3 = 1, kF16 = 2, kF32 = 3, kI8 = 6 };
+
+struct TensorView {
+  uint32_t dtype = 0, layout = 0, rank = 0, shape[4] = {0, 0, 0, 0};
+  const uint8_t* data = nullptr;
+  uint64_t bytes = 0;
+  uint64_t count() const {
+    uint64_t n = 1;
+    for (uint32_t d = 0; d < rank; ++d) n *= shape[d];
+    return n;
+  }
+  const float* f32() const { return reinterpret_cast<const float*>(data); }
+  const uint16_t* f16() const { return reinterpret_cast<const uint16_t*>(data); }
+};
+
+template <typename T>
+static T rd(const uint8_t* p, size_t off) {
+  T v;
+  std::memcpy(&v, p + off, sizeof(T));
+  return v;
+}
+static std::string fixed_string(const uint8_t* p, size_t n, const char* what) {
+  size_t len = 0;
+  while (len < n && p[len]) ++len;
+  if (len == n) fail(AEISU_ERR_ARTIFACT, std::string("unterminated SPYR8 ") + what);
+  for (size_t i = len; i < n; ++i)
+    if (p[i]) fail(AEISU_ERR_ARTIFACT, std::string("nonzero padding after SPYR8 ") + what);
+  return std::string(reinterpret_cast<const char*>(p), len);
+}
+static size_t elem_size(uint32_t dt) {
+  switch (dt) {
+    case kE4M3: return 1;
+    case kF16: return 2;
+    case kF32: return 4;
+    case kI8: return 1;
+    default: return 0;
+  }
+}
+
+struct Artifact {
+  std::vector<uint8_t> storage;
+  std::string checksum_hex;
+  std::unordered_map<std::string, TensorView> tensors;
+
+  bool has(const std::string& name) const { return tensors.count(name) != 0; }
+  const TensorView& need(const std::string& name, uint32_t dtype, std::initializer_list<uint32_t> shape) const {
+    auto it = tensors.find(name);
+    if (it == tensors.end()) fail(AEISU_ERR_ARTIFACT, "missing SPYR8 tensor: " + name);
+    const TensorView& t = it->second;
+    bool ok = t.dtype == dtype && t.rank == shape.size();
+    uint32_t d = 0;
+    for (uint32_t s : shape) ok = ok && t.shape[d++] == s;
+    if (!ok) fail(AEISU_ERR_ARTIFACT, "SPYR8 tensor has wrong type or shape: " + name);
+    return t;
+  }
+};
+
+static Artifact parse_artifact(const uint8_t* data, size_t size) {
+  Artifact a;
+  if (size < kHeaderSize) fail(AEISU_ERR_ARTIFACT, "SPYR8 artifact is smaller than its header");
+  a.storage.assign(data, data + size);
+  const uint8_t* p = a.storage.data();
+  static const char magic[8] = {'S', 'P', 'Y', 'R', '8', 'F', '8', '\0'};
+  if (std::memcmp(p, magic, 8) != 0 || rd<uint32_t>(p, 8) != 1 || rd<uint32_t>(p, 12) != kHeaderSize ||
+      rd<uint32_t>(p, 16) != 0x01020304u || rd<uint32_t>(p, 20) != 0)
+    fail(AEISU_ERR_ARTIFACT, "unsupported SPYR8 magic/version/endian/flags");
+  const std::string arch = fixed_string(p + 24, 64, "architecture");
+  if (arch != kArchitecture) fail(AEISU_ERR_ARTIFACT, "unsupported SPYR8 architecture: " + arch);
+  const uint32_t expect[14] = {8, 32, 32, 64, 4, 64, 2, 1, 1, 2, 1, 0, 64, 80};
+  for (int i = 0; i < 14; ++i) {
+    if (i == 11) continue;  // tensor count
+    if (rd<uint32_t>(p, 88 + 4 * i) != expect[i]) fail(AEISU_ERR_ARTIFACT, "unsupported or inconsistent SPYR8 header");
+  }
+  const uint32_t count = rd<uint32_t>(p, 132);
+  const float shift = rd<float>(p, 144), gain = rd<float>(p, 148);
+  const uint64_t file_size = rd<uint64_t>(p, 152), toc_off = rd<uint64_t>(p, 160), toc_bytes = rd<uint64_t>(p, 168),
+                 payload = rd<uint64_t>(p, 176);
+  const uint64_t toc_end = toc_off + toc_bytes;
+  if (file_size != size || toc_off != kHeaderSize || toc_bytes != uint64_t(count) * kDescSize ||
+      payload < ((toc_end + kAlign - 1) / kAlign) * kAlign || payload > file_size)
+    fail(AEISU_ERR_ARTIFACT, "unsupported or inconsistent SPYR8 header");
+  for (size_t i = 216; i < kHeaderSize; ++i)
+    if (p[i]) fail(AEISU_ERR_ARTIFACT, "nonzero SPYR8 v1 header extension bytes");
+  if (!std::isfinite(shift) || shift < 0 || !std::isfinite(gain) || gain < 0)
+    fail(AEISU_ERR_ARTIFACT, "invalid SPYR8 edge-phase parameters");
+  {
+    Sha256 h;
+    h.update(p, kChecksumOffset);
+    const uint8_t zeros[32] = {};
+    h.update(zeros, 32);
+    h.update(p + kChecksumOffset + 32, size - kChecksumOffset - 32);
+    const auto digest = h.finish();
+    char hex[65];
+    for (int i = 0; i < 32; ++i) std::snprintf(hex + 2 * i, 3, "%02x", digest[i]);
+    if (std::memcmp(digest.data(), p + kChecksumOffset, 32) != 0) {
+      char stored[65];
+      for (int i = 0; i < 32; ++i) std::snprintf(stored + 2 * i, 3, "%02x", p[kChecksumOffset + i]);
+      fail(AEISU_ERR_ARTIFACT, std::string("SPYR8 artifact checksum mismatch: expected ") + stored + ", observed " + hex);
+    }
+    a.checksum_hex = hex;
+  }
+  std::vector<std::pair<uint64_t, uint64_t>> ranges;
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint8_t* d = p + toc_off + uint64_t(i) * kDescSize;
+    const std::string name = fixed_string(d, 32, "tensor name");
+    TensorView t;
+    t.dtype = rd<uint32_t>(d, 32);
+    t.layout = rd<uint32_t>(d, 36);
+    t.rank = rd<uint32_t>(d, 40);
+    if (name.empty() || a.tensors.count(name) || t.rank == 0 || t.rank > 4)
+      fail(AEISU_ERR_ARTIFACT, "invalid or duplicate SPYR8 tensor descriptor");
+    uint64_t elements = 1;
+    for (int k = 0; k < 4; ++k) {
+      t.shape[k] = rd<uint32_t>(d, 44 + 4 * k);
+      if ((uint32_t)k < t.rank) {
+        if (t.shape[k] == 0 || elements > (uint64_t(1) << 40) / t.shape[k])
+          fail(AEISU_ERR_ARTIFACT, "invalid SPYR8 tensor dimensions: " + name);
+        elements *= t.shape[k];
+      } else if (t.shape[k] != 0) {
+        fail(AEISU_ERR_ARTIFACT, "nonzero unused SPYR8 dimension: " + name);
+      }
+    }
+    const size_t es = elem_size(t.dtype);
+    if (es == 0) fail(AEISU_ERR_ARTIFACT, "unsupported SPYR8 tensor data type: " + name);
+    const uint64_t off = rd<uint64_t>(d, 60), bytes = rd<uint64_t>(d, 68);
+    if (off % kAlign || off < payload || bytes == 0 || off > file_size || bytes > file_size - off ||
+        bytes != elements * es || rd<uint32_t>(d, 76) != 0)
+      fail(AEISU_ERR_ARTIFACT, "SPYR8 tensor bounds or byte count mismatch: " + name);
+    t.data = p + off;
+    t.bytes = bytes;
+    a.tensors.emplace(name, t);
+    ranges.emplace_back(off, off + bytes);
+  }
+  std::sort(ranges.begin(), ranges.end());
+  for (size_t i = 1; i < ranges.size(); ++i)
+    if (ranges[i - 1].second > ranges[i].first) fail(AEISU_ERR_ARTIFACT, "overlapping SPYR8 tensor payloads");
+  return a;
+}
+
+// ------------------------------------------------------------------------------------------------
+// fragment packing (operand register images; layout described in common.hpp)
+// ------------------------------------------------------------------------------------------------
+static uint16_t f32_to_f16_bits(float v) {
+  _Float16 h = (_Float16)v;
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+static float f16_bits_to_f32(uint16_t b) {
+  _Float16 h;
+  std::memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// out[(f*64 + lane)*E + i] = fn(f, m = lane & 15, slot = (lane >> 4)*E + i)
+template <typename T, typename Fn>
+static std::vector<T> pack_frags(int nfrag, int E, Fn fn) {
+  std::vector<T> out(size_t(nfrag) * 64 * E);
+  for (int f = 0; f < nfrag; ++f)
+    for (int lane = 0; lane < 64; ++lane)
+      for (int i = 0; i < E; ++i) out[(size_t(f) * 64 + lane) * E + i] = fn(f, lane & 15, (lane >> 4) * E + i);
+  return out;
+}
+
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  std::vector<uint8_t> staged;  // host image waiting for commit()
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  ~DeviceBuffer() { release(); }
+  void release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+  }
+  void alloc(size_t n) {
+    release();
+    if (n == 0) return;
+    check_hip(hipMalloc(&ptr, n), "hipMalloc");
+    bytes = n;
+  }
+  // Stage a host image; the device copy is made by commit() once every
+  // tensor of the artifact has been validated (no HIP call before that).
+  template <typename T>
+  void upload(const std::vector<T>& v) {
+    staged.resize(v.size() * sizeof(T));
+    std::memcpy(staged.data(), v.data(), staged.size());
+  }
+  void commit() {
+    if (staged.empty()) return;
+    alloc(staged.size());
+    check_hip(hipMemcpy(ptr, staged.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy(weights)");
+    staged.clear();
+    staged.shrink_to_fit();
+  }
+  template <typename T>
+  T* as() const { return reinterpret_cast<T*>(ptr); }
+};
+
+struct LayerDev {
+  DeviceBuffer frag, bias, scale;
+};
+
+// ------------------------------------------------------------------------------------------------
+// engine
+// ------------------------------------------------------------------------------------------------
+constexpr int kStageEvents = AEISU_STAGE_COUNT;  // 7 boundaries per frame (start + 6 stage ends)
+constexpr int kMaxTimedFrames = 4096;
+
+struct Runtime {
+  int device = 0, precision = 0, mode = 0, cu_count = 0;
+  bool project_precise = false;
+  std::string checksum;
+  float analysis[24];
+  float act[10] = {};
+  LayerDev project, compress, grouped[4], expand, refine_tail, head;
+  DeviceBuffer tail_bias;
+  // geometry
+  bool configured = false;
+  int batch = 0, H = 0, W = 0, Hp = 0, Wp = 0, py = 0, px = 0, Hq = 0, Wq = 0, Hl = 0, Wl = 0;
+  int in_fp32 = 0, out_fp32 = 0;
+  unsigned flags = 0;
+  DeviceBuffer skip, work, meta, nonfinite;
+  DeviceBuffer low[5];
+  int nlow = 2;
+  struct Grids { int project, compress, grouped, expand, refine, head; } grid{};
+  // captured frame graphs, one per (input, output) buffer pair (a small LRU-free cache)
+  struct Graph {
+    const void* in;
+    void* out;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+  };
+  static constexpr size_t kMaxGraphs = 16;
+  std::vector<Graph> graphs;
+  hipStream_t capture_stream = nullptr;
+  // timing
+  std::vector<hipEvent_t> events;  // kStageEvents per recorded frame
+  int timed_frames = 0;
+
+  ~Runtime() {
+    (void)hipSetDevice(device);
+    drop_graph();
+    for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    if (capture_stream) (void)hipStreamDestroy(capture_stream);
+  }
+  void drop_graph() {
+    for (Graph& g : graphs) {
+      (void)hipGraphExecDestroy(g.exec);
+      (void)hipGraphDestroy(g.graph);
+    }
+    graphs.clear();
+  }
+
+  size_t low_elem() const { return mode == 0 ? 2 : 1; }
+};
+
+static void require_prelu(const Artifact& a, const std::string& layer, uint32_t cout, float value) {
+  const TensorView& t = a.need(layer + ".prelu", kF32, {cout});
+  for (uint32_t i = 0; i < cout; ++i)
+    if (t.f32()[i] != value)
+      fail(AEISU_ERR_ARTIFACT, "unsupported per-channel slope in " + layer + ".prelu (kernels implement " +
+                                   std::to_string(value) + ")");
+}
+
+static std::vector<float> as_f32_vector(const TensorView& t) { return std::vector<float>(t.f32(), t.f32() + t.count()); }
+
+static void upload_weights(Runtime& rt, const Artifact& a) {
+  // --- shared tensors and contracts (SrcPyrModel.cpp:355-422)
+  const TensorView& stencil = a.need("analysis_stencil", kF32, {24});
+  for (int i = 0; i < 24; ++i) {
+    rt.analysis[i] = stencil.f32()[i];
+    if (!std::isfinite(rt.analysis[i])) fail(AEISU_ERR_ARTIFACT, "Nonfinite learned analysis 4-dir parameters");
+  }
+  const TensorView& base = a.need("adaptive_base", kF32, {25, 4});
+  const TensorView& basis = a.need("adaptive_basis", kF32, {25, 16, 4});
+  for (int i = 0; i < 100; ++i)
+    if (!std::isfinite(base.f32()[i])) fail(AEISU_ERR_ARTIFACT, "Nonfinite adaptive learned base");
+  for (int kp = 0; kp < 64; ++kp) {
+    float dc = 0, l1 = 0;
+    for (int tap = 0; tap < 25; ++tap) {
+      const float v = basis.f32()[tap * 64 + kp];
+      if (!std::isfinite(v)) fail(AEISU_ERR_ARTIFACT, "Nonfinite adaptive basis");
+      dc += v;
+      l1 += std::fabs(v);
+    }
+    if (std::fabs(dc) > 1e-5f || l1 > 0.5001f) fail(AEISU_ERR_ARTIFACT, "Adaptive basis violates zero-DC/L1 contract");
+  }
+  const TensorView& guards = a.need("precision_guards", kF32, {2});
+  for (int i = 0; i < 2; ++i)
+    if (guards.f32()[i] != 0.f && guards.f32()[i] != 1.f) fail(AEISU_ERR_ARTIFACT, "Invalid adaptive precision policy");
+  if (rt.mode != 0) {
+    const TensorView& s = a.need("activation_scales", kF32, {10});
+    for (int i = 0; i < 10; ++i) {
+      rt.act[i] = s.f32()[i];
+      if (!std::isfinite(rt.act[i]) || rt.act[i] <= 0) fail(AEISU_ERR_ARTIFACT, "invalid activation scale");
+    }
+  }
+
+  // --- FP16 layers used by every policy: project, refine, tail
+  auto w16 = [&](const std::string& l, std::initializer_list<uint32_t> shape) {
+    return a.need(l + ".weight_fp16", kF16, shape).f16();
+  };
+  auto bias = [&](const std::string& l, uint32_t cout) { return as_f32_vector(a.need(l + ".bias", kF32, {cout})); };
+  {
+    // FP16 policy: hi/lo split operands (fragments hi T0, hi T1, lo T0, lo T1); the FP32
+    // weights come from project.weight_fp32 when the artifact carries them.  Mixed / INT8:
+    // FP16 weights as in the reference deployment (SrcPyrCudaRuntime.cu:2536-2566).
+    const uint16_t* w = w16("project", {32, 32, 1, 1});
+    require_prelu(a, "project", 32, 0.1f);
+    rt.project_precise = rt.mode == 0;
+    const float* w32 = nullptr;
+    if (rt.project_precise && a.has("project.weight_fp32")) w32 = a.need("project.weight_fp32", kF32, {32, 32, 1, 1}).f32();
+    rt.project.frag.upload(pack_frags<uint16_t>(rt.project_precise ? 4 : 2, 8, [&](int f, int m, int s) -> uint16_t {
+      const int idx = (16 * (f & 1) + m) * 32 + s;
+      if (!w32) return f < 2 ? w[idx] : (uint16_t)0;
+      const uint16_t hi = f32_to_f16_bits(w32[idx]);
+      return f < 2 ? hi : f32_to_f16_bits(w32[idx] - f16_bits_to_f32(hi));
+    }));
+    rt.project.bias.upload(bias("project", 32));
+  }
+  {
+    const uint16_t* wr = w16("refine", {64, 32, 3, 3});
+    const uint16_t* wt = w16("tail", {64, 64, 1, 1});
+    require_prelu(a, "refine", 64, 0.1f);
+    require_prelu(a, "tail", 64, 1.0f);
+    auto img = pack_frags<uint16_t>(36, 8, [&](int f, int m, int s) {
+      const int T = f / 9, tap = f % 9;
+      return wr[((16 * T + m) * 32 + s) * 9 + tap];
+    });
+    auto tail = pack_frags<uint16_t>(8, 8, [&](int f, int m, int s) {
+      const int T = f / 2, k = f % 2, g = s / 8, i = s % 8;
+      return wt[(16 * T + m) * 64 + 16 * (2 * k + i / 4) + 4 * g + (i % 4)];
+    });
+    img.insert(img.end(), tail.begin(), tail.end());
+    rt.refine_tail.frag.upload(img);
+    rt.refine_tail.bias.upload(bias("refine", 64));
+    std::vector<float> tb = bias("tail", 64);
+    for (float& v : tb) v = f16_bits_to_f32(f32_to_f16_bits(v));  // FP16-rounded tail bias (SrcPyrNativeFp16Refine.cuh:494-495)
+    rt.tail_bias.upload(tb);
+  }
+
+  // --- low-resolution body
+  static const char* bodies[6] = {"compress", "bottleneck0", "bottleneck1", "bottleneck2", "bottleneck3", "expand"};
+  for (int li = 0; li < 6; ++li) {
+    const std::string l = bodies[li];
+    const bool grp = li >= 1 && li <= 4;
+    const uint32_t cout = li == 0 ? 64 : (li == 5 ? 128 : 64);
+    const uint32_t cin = li == 0 ? 128 : (li == 5 ? 64 : 32);
+    const uint32_t ks = grp ? 3 : 1;
+    LayerDev& dst = li == 0 ? rt.compress : (li == 5 ? rt.expand : rt.grouped[li - 1]);
+    require_prelu(a, l, cout, 0.1f);
+    // generic element fetch W[o][i][tap] from whichever storage the policy uses
+    if (rt.mode == 0 || rt.mode == 1) {
+      const bool fp8 = rt.mode == 1;
+      const uint8_t* codes = fp8 ? a.need(l + ".weight_fp8", kE4M3, {cout, cin, ks, ks}).data : nullptr;
+      const uint16_t* half = fp8 ? nullptr : a.need(l + ".weight_fp16", kF16, {cout, cin, ks, ks}).f16();
+      auto W = [&](int o, int i, int tap) -> uint32_t {
+        const size_t idx = (size_t(o) * cin + i) * ks * ks + tap;
+        return fp8 ? codes[idx] : half[idx];
+      };
+      std::function<uint32_t(int, int, int)> fn;
+      int nfrag = 0;
+      if (li == 0) {
+        nfrag = 16;  // f = T*4 + kappa(phase); slot s = skip channel c
+        fn = [&](int f, int m, int s) { return W(16 * (f / 4) + m, s * 4 + (f % 4), 0); };
+      } else if (li == 5) {
+        nfrag = 16;  // f = T*2 + kappa; row m of tile T = channel c of phase T&3
+        fn = [&](int f, int m, int s) {
+          const int T = f / 2, k = f % 2, o = (16 * (T >> 2) + m) * 4 + (T & 3);
+          return W(o, 32 * k + s, 0);
+        };
+      } else {
+        nfrag = 36;  // f = (group*2 + T)*9 + tap
+        fn = [&](int f, int m, int s) {
+          const int gt = f / 9, tap = f % 9;
+          return W(32 * (gt / 2) + 16 * (gt % 2) + m, s, tap);
+        };
+      }
+      if (fp8) dst.frag.upload(pack_frags<uint8_t>(nfrag, 8, [&](int f, int m, int s) { return (uint8_t)fn(f, m, s); }));
+      else dst.frag.upload(pack_frags<uint16_t>(nfrag, 8, [&](int f, int m, int s) { return (uint16_t)fn(f, m, s); }));
+      if (fp8) {
+        const int s_in = li == 0 ? 1 : li + 1;  // compress s1, bottleneck i s(i+2), expand s6
+        const TensorView& ws = a.need(l + ".weight_scale", kF32, {cout});
+        std::vector<float> sc(cout);
+        for (uint32_t c = 0; c < cout; ++c) sc[c] = rt.act[s_in] * ws.f32()[c];
+        dst.scale.upload(sc);
+        dst.bias.upload(as_f32_vector(a.need(l + ".bias_fp8", kF32, {cout})));
+      } else {
+        dst.bias.upload(bias(l, cout));
+      }
+    } else {
+      const int8_t* q = reinterpret_cast<const int8_t*>(a.need(l + ".weight_i8", kI8, {cout, cin, ks, ks}).data);
+      auto W = [&](int o, int i, int tap) -> int8_t { return q[(size_t(o) * cin + i) * ks * ks + tap]; };
+      std::vector<int8_t> img;
+      if (li == 0) {
+        img = pack_frags<int8_t>(8, 16, [&](int f, int m, int s) {  // f = T*2 + k
+          const int T = f / 2, k = f % 2, g = s / 16, i = s % 16;
+          const int ph = 2 * k + (g >> 1), c = 16 * (g & 1) + i;
+          return W(16 * T + m, c * 4 + ph, 0);
+        });
+      } else if (li == 5) {
+        img = pack_frags<int8_t>(8, 16, [&](int T, int m, int s) {
+          return W((16 * (T >> 2) + m) * 4 + (T & 3), s, 0);
+        });
+      } else {
+        img = pack_frags<int8_t>(20, 16, [&](int f, int m, int s) {  // f = (group*2 + T)*5 + k
+          const int gt = f / 5, k = f % 5, g = s / 16, i = s % 16;
+          const int tap = 2 * k + (g >> 1), c = 16 * (g & 1) + i;
+          return tap > 8 ? (int8_t)0 : W(32 * (gt / 2) + 16 * (gt % 2) + m, c, tap);
+        });
+      }
+      dst.frag.upload(img);
+      dst.scale.upload(as_f32_vector(a.need(l + ".int8_factor", kF32, {cout})));
+      dst.bias.upload(bias(l, cout));
+    }
+  }
+
+  // --- head bank: [K_hi | K_lo] and [K_hi | base_hi, base_lo] fragments, rows tap*4 + phase
+  {
+    const float* K = basis.f32();  // [25][16][4]
+    const float* B = base.f32();   // [25][4]
+    auto hi = [](float v) { return f32_to_f16_bits(v); };
+    auto lo = [](float v) { return f32_to_f16_bits(v - f16_bits_to_f32(f32_to_f16_bits(v))); };
+    rt.head.frag.upload(pack_frags<uint16_t>(14, 8, [&](int f, int m, int s) -> uint16_t {
+      const int t = f % 7, row = 16 * t + m, tap = row / 4, ph = row % 4;
+      if (tap >= 25) return 0;
+      if (f < 7) return s < 16 ? hi(K[(tap * 16 + s) * 4 + ph]) : lo(K[(tap * 16 + s - 16) * 4 + ph]);
+      if (s < 16) return hi(K[(tap * 16 + s) * 4 + ph]);
+      if (s == 16) return hi(B[tap * 4 + ph]);
+      if (s == 17) return lo(B[tap * 4 + ph]);
+      return 0;
+    }));
+  }
+}
+
+static void commit_weights(Runtime& rt) {
+  for (LayerDev* l : {&rt.project, &rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3],
+                      &rt.expand, &rt.refine_tail, &rt.head}) {
+    l->frag.commit();
+    l->bias.commit();
+    l->scale.commit();
+  }
+  rt.tail_bias.commit();
+}
+
+static int clamp_grid(int tiles, int per_cu, int cus) {
+  int g = std::min(tiles, std::max(1, per_cu) * cus);
+  if (g >= 8) g -= g % 8;
+  return std::max(g, 1);
+}
+
+static void configure(Runtime& rt, int batch, int height, int width, int in_layout, int out_layout, unsigned flags) {
+  if (batch <= 0 || height <= 0 || width <= 0) fail(AEISU_ERR_INVALID_ARGUMENT, "batch, height and width must be positive");
+  if (height > 8192 || width > 8192 || batch > 1024) fail(AEISU_ERR_INVALID_ARGUMENT, "frame dimensions exceed 8192 (or batch > 1024)");
+  if ((in_layout != AEISU_LAYOUT_NCHW_F16 && in_layout != AEISU_LAYOUT_NCHW_F32) ||
+      (out_layout != AEISU_LAYOUT_NCHW_F16 && out_layout != AEISU_LAYOUT_NCHW_F32))
+    fail(AEISU_ERR_INVALID_ARGUMENT, "unsupported frame layout");
+  if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD))
+    fail(AEISU_ERR_INVALID_ARGUMENT, "unknown configure flag");
+  const bool no_pad = flags & AEISU_FLAG_NO_PAD;
+  if (no_pad && (height % 4 || width % 4))
+    fail(AEISU_ERR_INVALID_ARGUMENT, "Source H/W must be divisible by 4");
+  rt.drop_graph();
+  rt.configured = false;
+  rt.batch = batch;
+  rt.H = height;
+  rt.W = width;
+  if (no_pad) {
+    // The caller passes a frame that is already on the padded grid (aeisu/model.py:473-479).
+    rt.py = rt.px = 0;
+    rt.Hp = height;
+    rt.Wp = width;
+  } else {
+    // align32 + halo16 replicate padding (aeisu/runtime.py:82-84), realised by clamped reads.
+    const int ey = (32 - height % 32) % 32, ex = (32 - width % 32) % 32;
+    rt.py = 16 + ey / 2;
+    rt.px = 16 + ex / 2;
+    rt.Hp = height + 32 + ey;
+    rt.Wp = width + 32 + ex;
+  }
+  rt.Hq = rt.Hp / 2;
+  rt.Wq = rt.Wp / 2;
+  rt.Hl = rt.Hp / 4;
+  rt.Wl = rt.Wp / 4;
+  rt.in_fp32 = in_layout == AEISU_LAYOUT_NCHW_F32;
+  rt.out_fp32 = out_layout == AEISU_LAYOUT_NCHW_F32;
+  rt.flags = flags;
+  const size_t packed = size_t(batch) * rt.Hq * rt.Wq, lowpx = size_t(batch) * rt.Hl * rt.Wl;
+  rt.skip.alloc(packed * 32 * 2);
+  rt.work.alloc(packed * 32 * 2);
+  rt.meta.alloc(packed * 64 * 2);
+  rt.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : 2;
+  for (int i = 0; i < 5; ++i) {
+    if (i < rt.nlow) rt.low[i].alloc(lowpx * 64 * rt.low_elem());
+    else rt.low[i].release();
+  }
+  rt.nonfinite.alloc(4);
+  check_hip(hipMemset(rt.nonfinite.ptr, 0, 4), "hipMemset(flag)");
+  const int m = rt.mode, cus = rt.cu_count;
+  const int low_groups = batch * rt.Hl * ((rt.Wl + 15) / 16);
+  rt.grid.project = clamp_grid(project_num_tiles(batch, rt.Hq, rt.Wq), project_blocks_per_cu(rt.in_fp32, rt.project_precise), cus);
+  rt.grid.compress = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(0, m), cus);
+  rt.grid.grouped = clamp_grid(grouped_num_tiles(batch, rt.Hl, rt.Wl), body_blocks_per_cu(1, m), cus);
+  rt.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, m), cus);
+  rt.grid.refine = clamp_grid(refine_num_tiles(batch, rt.Hq, rt.Wq), refine_blocks_per_cu(), cus);
+  rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
+  rt.configured = true;
+}
+
+static float inv(float s) { return 1.0f / s; }
+
+// Low-buffer slot written by body layer li (0 compress, 1..4 bottlenecks).
+static int low_slot(const Runtime& rt, int li) { return rt.nlow == 5 ? li : (li % 2); }
+
+static void enqueue_controller(Runtime& rt, const void* d_in, void* d_meta, hipStream_t s, hipEvent_t* ev) {
+  const int m = rt.mode;
+  if (ev) check_hip(hipEventRecord(ev[0], s), "hipEventRecord");
+  check_hip(launch_project(rt.in_fp32, rt.project_precise, d_in, rt.project.frag.ptr, rt.project.bias.as<float>(), rt.skip.ptr, rt.analysis,
+                           rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.grid.project, s), "project launch");
+  if (ev) check_hip(hipEventRecord(ev[1], s), "hipEventRecord");
+  const float* A = rt.act;
+  check_hip(launch_compress(m, rt.skip.ptr, rt.compress.frag.ptr, rt.compress.bias.as<float>(),
+                            rt.compress.scale.as<float>(), rt.low[low_slot(rt, 0)].ptr, m ? inv(A[1]) : 0.f,
+                            m ? inv(A[2]) : 0.f, rt.Hl, rt.Wl, rt.batch, rt.grid.compress, s), "compress launch");
+  if (ev) check_hip(hipEventRecord(ev[2], s), "hipEventRecord");
+  for (int i = 0; i < 4; ++i) {
+    check_hip(launch_grouped(m, rt.low[low_slot(rt, i)].ptr, rt.grouped[i].frag.ptr, rt.grouped[i].bias.as<float>(),
+                             rt.grouped[i].scale.as<float>(), rt.low[low_slot(rt, i + 1)].ptr, m ? inv(A[i + 3]) : 0.f,
+                             rt.Hl, rt.Wl, rt.batch, rt.grid.grouped, s), "bottleneck launch");
+  }
+  if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
+  check_hip(launch_expand(m, rt.low[low_slot(rt, 4)].ptr, rt.skip.ptr, rt.expand.frag.ptr, rt.expand.bias.as<float>(),
+                          rt.expand.scale.as<float>(), rt.work.ptr, m ? inv(A[7]) : 0.f, m ? A[7] : 0.f, rt.Hl, rt.Wl,
+                          rt.batch, rt.grid.expand, s), "expand launch");
+  if (ev) check_hip(hipEventRecord(ev[4], s), "hipEventRecord");
+  check_hip(launch_refine_tail(rt.work.ptr, rt.refine_tail.frag.ptr, rt.refine_tail.bias.as<float>(),
+                               rt.tail_bias.as<float>(), d_meta, rt.Hq, rt.Wq, rt.batch, rt.grid.refine, s),
+            "refine/tail launch");
+  if (ev) check_hip(hipEventRecord(ev[5], s), "hipEventRecord");
+}
+
+static void enqueue_head(Runtime& rt, const void* d_in, const void* d_meta, void* d_out, hipStream_t s) {
+  check_hip(launch_head(rt.in_fp32, rt.out_fp32, d_in, d_meta, rt.head.frag.ptr, d_out, rt.H, rt.W, rt.Hq, rt.Wq,
+                        rt.py, rt.px, rt.batch, rt.nonfinite.as<unsigned>(), rt.grid.head, s), "head launch");
+}
+
+static hipEvent_t* next_events(Runtime& rt) {
+  if (!(rt.flags & AEISU_FLAG_STAGE_TIMING) || rt.timed_frames >= kMaxTimedFrames) return nullptr;
+  const size_t need = size_t(rt.timed_frames + 1) * kStageEvents;
+  while (rt.events.size() < need) {
+    hipEvent_t e;
+    check_hip(hipEventCreate(&e), "hipEventCreate");
+    rt.events.push_back(e);
+  }
+  return &rt.events[size_t(rt.timed_frames++) * kStageEvents];
+}
+
+static void enqueue_frame(Runtime& rt, const void* d_in, void* d_out, hipStream_t s, hipEvent_t* ev) {
+  enqueue_controller(rt, d_in, rt.meta.ptr, s, ev);
+  enqueue_head(rt, d_in, rt.meta.ptr, d_out, s);
+  if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
+}
+
+static void require_configured(const Runtime& rt) {
+  if (!rt.configured) fail(AEISU_ERR_STATE, "runtime is not configured");
+}
+
+}  // namespace aeisu
+
+// ================================================================================================
+// C ABI
+// ================================================================================================
+using aeisu::Error;
+using aeisu::Runtime;
+
+struct aeisu_runtime {
+  std::unique_ptr<Runtime> impl;
+};
+
+static thread_local std::string g_last_error;
+
+template <typename Fn>
+static int guarded(Fn fn) {
+  try {
+    fn();
+    g_last_error.clear();
+    return AEISU_OK;
+  } catch (const Error& e) {
+    g_last_error = e.what();
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return AEISU_ERR_HIP;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return AEISU_ERR_HIP;
+  }
+}
+
+static Runtime& runtime_of(aeisu_runtime* rt) {
+  if (!rt || !rt->impl) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null runtime handle");
+  aeisu::check_hip(hipSetDevice(rt->impl->device), "hipSetDevice");
+  return *rt->impl;
+}
+
+static int create_impl(const uint8_t* data, size_t size, int precision, aeisu_runtime** out) {
+  return guarded([&] {
+    if (!out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    if (!data || size == 0) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "empty artifact");
+    if (precision != AEISU_PRECISION_FP16 && precision != AEISU_PRECISION_MIXED && precision != AEISU_PRECISION_INT8)
+      aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "unknown precision");
+    auto rt = std::make_unique<Runtime>();
+    rt->precision = precision;
+    rt->mode = precision == AEISU_PRECISION_FP16 ? 0 : (precision == AEISU_PRECISION_MIXED ? 1 : 2);
+    {
+      // host-only: parse, validate and pack every tensor before touching the device
+      aeisu::Artifact art = aeisu::parse_artifact(data, size);
+      rt->checksum = art.checksum_hex;
+      aeisu::upload_weights(*rt, art);
+    }
+    aeisu::check_hip(hipGetDevice(&rt->device), "hipGetDevice");
+    hipDeviceProp_t prop;
+    aeisu::check_hip(hipGetDeviceProperties(&prop, rt->device), "hipGetDeviceProperties");
+    rt->cu_count = prop.multiProcessorCount;
+    aeisu::commit_weights(*rt);
+    auto* h = new aeisu_runtime;
+    h->impl = std::move(rt);
+    *out = h;
+  });
+}
+
+extern "C" {
+
+int aeisu_create_from_memory(const void* data, size_t size, int precision, aeisu_runtime** out) {
+  return create_impl(static_cast<const uint8_t*>(data), size, precision, out);
+}
+
+int aeisu_create_from_file(const char* path, int precision, aeisu_runtime** out) {
+  std::vector<uint8_t> bytes;
+  const int rc = guarded([&] {
+    if (!path) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null path");
+    std::ifstream f(path, std::ios::binary | std::ios::ate);
+    if (!f) aeisu::fail(AEISU_ERR_ARTIFACT, std::string("could not open SPYR8 model: ") + path);
+    const std::streamsize n = f.tellg();
+    f.seekg(0);
+    bytes.resize(size_t(std::max<std::streamsize>(n, 0)));
+    if (n <= 0 || !f.read(reinterpret_cast<char*>(bytes.data()), n))
+      aeisu::fail(AEISU_ERR_ARTIFACT, "failed to read complete SPYR8 artifact");
+  });
+  if (rc != AEISU_OK) {
+    if (out) *out = nullptr;
+    return rc;
+  }
+  return create_impl(bytes.data(), bytes.size(), precision, out);
+}
+
+int aeisu_configure(aeisu_runtime* h, int batch, int height, int width, int in_layout, int out_layout, unsigned flags) {
+  return guarded([&] { aeisu::configure(runtime_of(h), batch, height, width, in_layout, out_layout, flags); });
+}
+
+int aeisu_upscale_async(aeisu_runtime* h, const void* d_in, void* d_out, void* stream) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    aeisu::require_configured(rt);
+    if (!d_in || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null frame buffer");
+    aeisu::enqueue_frame(rt, d_in, d_out, (hipStream_t)stream, aeisu::next_events(rt));
+  });
+}
+
+int aeisu_check_finite(aeisu_runtime* h, void* stream) {
+  int status = AEISU_OK;
+  const int rc = guarded([&] {
+    Runtime& rt = runtime_of(h);
+    aeisu::require_configured(rt);
+    unsigned flag = 0;
+    aeisu::check_hip(hipMemcpyAsync(&flag, rt.nonfinite.ptr, 4, hipMemcpyDeviceToHost, (hipStream_t)stream), "flag readback");
+    aeisu::check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+    if (flag) {
+      aeisu::check_hip(hipMemsetAsync(rt.nonfinite.ptr, 0, 4, (hipStream_t)stream), "flag reset");
+      aeisu::check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+      status = AEISU_ERR_NONFINITE;
+    }
+  });
+  if (rc != AEISU_OK) return rc;
+  if (status != AEISU_OK) g_last_error = "Non-finite model reconstruction";
+  return status;
+}
+
+int aeisu_upscale(aeisu_runtime* h, const void* d_in, void* d_out, void* stream) {
+  const int rc = aeisu_upscale_async(h, d_in, d_out, stream);
+  if (rc != AEISU_OK) return rc;
+  return aeisu_check_finite(h, stream);
+}
+
+int aeisu_upscale_graph(aeisu_runtime* h, const void* d_in, void* d_out, void* stream) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    aeisu::require_configured(rt);
+    if (!d_in || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null frame buffer");
+    hipGraphExec_t exec = nullptr;
+    for (const auto& g : rt.graphs)
+      if (g.in == d_in && g.out == d_out) exec = g.exec;
+    if (!exec) {
+      if (rt.graphs.size() >= Runtime::kMaxGraphs) rt.drop_graph();
+      if (!rt.capture_stream)
+        aeisu::check_hip(hipStreamCreateWithFlags(&rt.capture_stream, hipStreamNonBlocking), "hipStreamCreate");
+      aeisu::check_hip(hipStreamBeginCapture(rt.capture_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      hipGraph_t graph = nullptr;
+      try {
+        aeisu::enqueue_frame(rt, d_in, d_out, rt.capture_stream, nullptr);
+      } catch (...) {
+        (void)hipStreamEndCapture(rt.capture_stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+      }
+      aeisu::check_hip(hipStreamEndCapture(rt.capture_stream, &graph), "hipStreamEndCapture");
+      const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        aeisu::check_hip(e, "hipGraphInstantiate");
+      }
+      rt.graphs.push_back({d_in, d_out, graph, exec});
+    }
+    aeisu::check_hip(hipGraphLaunch(exec, (hipStream_t)stream), "hipGraphLaunch");
+  });
+}
+
+int aeisu_controller_async(aeisu_runtime* h, const void* d_in, void* d_meta, void* stream) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    aeisu::require_configured(rt);
+    if (!d_in || !d_meta) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null buffer");
+    aeisu::enqueue_controller(rt, d_in, d_meta, (hipStream_t)stream, nullptr);
+  });
+}
+
+int aeisu_head_async(aeisu_runtime* h, const void* d_in, const void* d_meta, void* d_out, void* stream) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    aeisu::require_configured(rt);
+    if (!d_in || !d_meta || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null buffer");
+    aeisu::enqueue_head(rt, d_in, d_meta, d_out, (hipStream_t)stream);
+  });
+}
+
+size_t aeisu_intermediate_bytes(const aeisu_runtime* h, int which) {
+  if (!h || !h->impl || !h->impl->configured) return 0;
+  const Runtime& rt = *h->impl;
+  const size_t packed = size_t(rt.batch) * rt.Hq * rt.Wq, lowpx = size_t(rt.batch) * rt.Hl * rt.Wl;
+  if (which == AEISU_BUF_SKIP || which == AEISU_BUF_WORK) return packed * 64;
+  if (which == AEISU_BUF_META) return packed * 128;
+  if (which >= AEISU_BUF_LOW0 && which <= AEISU_BUF_LOW4) return lowpx * 64 * rt.low_elem();
+  return 0;
+}
+
+int aeisu_copy_intermediate(aeisu_runtime* h, int which, void* d_dst, size_t bytes, void* stream) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    aeisu::require_configured(rt);
+    const size_t need = aeisu_intermediate_bytes(h, which);
+    if (need == 0 || bytes != need || !d_dst) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "bad intermediate id, size or pointer");
+    const void* src = nullptr;
+    if (which == AEISU_BUF_SKIP) src = rt.skip.ptr;
+    else if (which == AEISU_BUF_WORK) src = rt.work.ptr;
+    else if (which == AEISU_BUF_META) src = rt.meta.ptr;
+    else {
+      const int li = which - AEISU_BUF_LOW0;
+      if (rt.nlow != 5 && li != 4) aeisu::fail(AEISU_ERR_STATE, "configure with AEISU_FLAG_KEEP_INTERMEDIATES to read this layer");
+      src = rt.low[aeisu::low_slot(rt, li)].ptr;
+    }
+    aeisu::check_hip(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "hipMemcpyAsync");
+  });
+}
+
+int aeisu_geometry(const aeisu_runtime* h, int out[6]) {
+  return guarded([&] {
+    if (!h || !h->impl || !out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null argument");
+    const Runtime& rt = *h->impl;
+    aeisu::require_configured(rt);
+    out[0] = rt.Hp; out[1] = rt.Wp; out[2] = rt.py; out[3] = rt.px; out[4] = rt.Hq; out[5] = rt.Wq;
+  });
+}
+
+int aeisu_stage_timings(aeisu_runtime* h, float ms[AEISU_STAGE_COUNT], int* frames) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    if (!ms) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output");
+    double acc[AEISU_STAGE_COUNT] = {};
+    for (int f = 0; f < rt.timed_frames; ++f) {
+      hipEvent_t* e = &rt.events[size_t(f) * aeisu::kStageEvents];
+      aeisu::check_hip(hipEventSynchronize(e[6]), "hipEventSynchronize");
+      for (int s = 0; s < 6; ++s) {
+        float t = 0;
+        aeisu::check_hip(hipEventElapsedTime(&t, e[s], e[s + 1]), "hipEventElapsedTime");
+        acc[s] += t;
+      }
+      float total = 0;
+      aeisu::check_hip(hipEventElapsedTime(&total, e[0], e[6]), "hipEventElapsedTime");
+      acc[AEISU_STAGE_TOTAL] += total;
+    }
+    for (int s = 0; s < AEISU_STAGE_COUNT; ++s) ms[s] = rt.timed_frames ? float(acc[s] / rt.timed_frames) : 0.f;
+    if (frames) *frames = rt.timed_frames;
+  });
+}
+
+int aeisu_reset_timings(aeisu_runtime* h) {
+  return guarded([&] { runtime_of(h).timed_frames = 0; });
+}
+
+size_t aeisu_persistent_bytes(const aeisu_runtime* h) {
+  if (!h || !h->impl) return 0;
+  const Runtime& rt = *h->impl;
+  size_t n = rt.project.frag.bytes + rt.project.bias.bytes + rt.compress.frag.bytes + rt.compress.bias.bytes +
+             rt.compress.scale.bytes + rt.expand.frag.bytes + rt.expand.bias.bytes + rt.expand.scale.bytes +
+             rt.refine_tail.frag.bytes + rt.refine_tail.bias.bytes + rt.tail_bias.bytes + rt.head.frag.bytes +
+             rt.skip.bytes + rt.work.bytes + rt.meta.bytes + rt.nonfinite.bytes;
+  for (const auto& g : rt.grouped) n += g.frag.bytes + g.bias.bytes + g.scale.bytes;
+  for (const auto& l : rt.low) n += l.bytes;
+  return n;
+}
+
+int aeisu_artifact_checksum(const aeisu_runtime* h, char out[65]) {
+  return guarded([&] {
+    if (!h || !h->impl || !out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null argument");
+    std::snprintf(out, 65, "%s", h->impl->checksum.c_str());
+  });
+}
+
+void aeisu_destroy(aeisu_runtime* h) { delete h; }
+
+const char* aeisu_last_error(void) { return g_last_error.c_str(); }
+
+const char* aeisu_version(void) { return "aeisu_amd 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,199 @@
+// Analysis features + pixel_unshuffle + project 1x1 (32 -> 32) + LeakyReLU,
+// producing the FP16 skip tensor at packed (half) resolution.
+//
+// Reference: aeisu/model.py:273-341 (_rgb_to_feature8), 481 (unshuffle,
+// project_540, LeakyReLU); native FusedPackRgbYLearnedRgb4DirAndProjectKernel,
+// optimized/native/src/neural/srcpyr/SrcPyrCudaRuntime.cu:2208-2219, 2360-2584.
+// Learned RGB and luma use explicitly unfused multiplies and adds in the
+// reference's evaluation order, and the directional stencils are evaluated
+// without contraction too, so the FP16-rounded features equal those of the
+// FP32 PyTorch model evaluated on the same input.
+//
+// Geometry: packed pixel (qy, qx) covers padded LR pixels (2qy+i, 2qx+j),
+// phase 2i+j, channel = feature*4 + phase; padded LR (Y, X) reads source
+// (clamp(Y-py), clamp(X-px)) -- the replicate padding of aeisu/runtime.py:84.
+//
+// gfx950 mapping: a block computes an 8x32 packed tile.  Luma of the
+// 18x66 LR halo region goes to LDS; each thread forms the 32 features of one
+// packed pixel into an LDS row; each wave then runs MFMAs (16x16x32 f16) per
+// 16 pixels against register-resident project weights.
+//
+// Two precisions:
+//  * PRECISE = false (Mixed / INT8 policies): features and weights rounded to
+//    FP16 exactly like the reference deployment, 2 MFMAs per 16 pixels.
+//  * PRECISE = true (FP16 policy): the project weights reach |w| ~ 31 with
+//    heavy cancellation, so FP16 operands alone cost ~4e-3 of output error.
+//    Features and weights are split into FP16 hi + lo parts and the product
+//    is formed as W_hi f_hi + W_lo f_hi + W_hi f_lo (6 MFMAs, FP32 accumulate),
+//    accurate to ~2^-22 relative.
+#include "common.hpp"
+
+namespace aeisu {
+
+struct Analysis {
+  float basis[9], mix[3], dx[3], dy[3], d45[3], d135[3];
+};
+
+constexpr int kPTW = 32, kPTH = 8;
+constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
+constexpr int kPFeat = 72;  // halves per LDS feature row: 32 hi + 32 lo + 8 pad
+
+template <typename Tin>
+__device__ __forceinline__ float3 rgb_at(const Tin* s, size_t plane, int W, int y, int x) {
+  const size_t o = (size_t)y * W + x;
+  return make_float3((float)s[o], (float)s[plane + o], (float)s[2 * plane + o]);
+}
+
+__device__ __forceinline__ float dot3_unfused(float3 v, float a, float b, float c) {
+  return __fadd_rn(__fadd_rn(__fmul_rn(v.x, a), __fmul_rn(v.y, b)), __fmul_rn(v.z, c));
+}
+// (p*a + q*b) + r*c, unfused, reference order
+__device__ __forceinline__ float comb3(float p, float a, float q, float b, float r, float c) {
+  return __fadd_rn(__fadd_rn(__fmul_rn(p, a), __fmul_rn(q, b)), __fmul_rn(r, c));
+}
+
+template <typename Tin, bool PRECISE>
+__global__ __launch_bounds__(256) void project_kernel(
+    const Tin* __restrict__ src, const h8* __restrict__ wfrag, const float* __restrict__ bias,
+    _Float16* __restrict__ skip, Analysis an, int H, int W, int Hq, int Wq, int py, int px, int batch) {
+  __shared__ float luma[kPLH][kPLW + 1];
+  __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat];
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const h8 A0 = wfrag[lane], A1 = wfrag[64 + lane];
+  h8 L0 = {}, L1 = {};
+  if constexpr (PRECISE) {
+    L0 = wfrag[128 + lane];
+    L1 = wfrag[192 + lane];
+  }
+  float bs[2][4];
+#pragma unroll
+  for (int T = 0; T < 2; ++T)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) bs[T][r] = bias[16 * T + 4 * g + r];
+  const size_t plane = (size_t)H * W;
+  const int tiles_x = (Wq + kPTW - 1) / kPTW, tiles_y = (Hq + kPTH - 1) / kPTH;
+  const int num_tiles = batch * tiles_x * tiles_y;
+  const int iters = tile_iters(num_tiles);
+  for (int it = 0; it < iters; ++it) {
+    const int tidx = tile_of(it, num_tiles);
+    if (tidx >= num_tiles) break;
+    const int b = tidx / (tiles_x * tiles_y);
+    const int rem = tidx - b * tiles_x * tiles_y;
+    const int qy0 = (rem / tiles_x) * kPTH, qx0 = (rem % tiles_x) * kPTW;
+    const Tin* s = src + (size_t)b * 3 * plane;
+    const int Y0 = 2 * qy0 - 1, X0 = 2 * qx0 - 1;   // padded LR origin of the luma halo
+    __syncthreads();
+    for (int q = tid; q < kPLH * kPLW; q += 256) {
+      const int r = q / kPLW, c = q - r * kPLW;
+      const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + c - px, 0), W - 1);
+      luma[r][c] = dot3_unfused(rgb_at(s, plane, W, sy, sx), an.mix[0], an.mix[1], an.mix[2]);
+    }
+    __syncthreads();
+    {
+      const int ty = tid / kPTW, tx = tid - ty * kPTW;
+      float f[8][4];
+#pragma unroll
+      for (int ph = 0; ph < 4; ++ph) {
+        const int i = ph >> 1, j = ph & 1;
+        const int Y = 2 * (qy0 + ty) + i, X = 2 * (qx0 + tx) + j;
+        const int sy = min(max(Y - py, 0), H - 1), sx = min(max(X - px, 0), W - 1);
+        const float3 v = rgb_at(s, plane, W, sy, sx);
+        f[0][ph] = dot3_unfused(v, an.basis[0], an.basis[1], an.basis[2]);
+        f[1][ph] = dot3_unfused(v, an.basis[3], an.basis[4], an.basis[5]);
+        f[2][ph] = dot3_unfused(v, an.basis[6], an.basis[7], an.basis[8]);
+        const int r = 2 * ty + i + 1, c = 2 * tx + j + 1;   // centre in the luma tile
+        const float ul = luma[r - 1][c - 1], uc = luma[r - 1][c], ur = luma[r - 1][c + 1];
+        const float cl = luma[r][c - 1], cc = luma[r][c], cr = luma[r][c + 1];
+        const float dl = luma[r + 1][c - 1], dc = luma[r + 1][c], dr = luma[r + 1][c + 1];
+        const float hmid = __fsub_rn(cr, cl), vmid = __fsub_rn(dc, uc);
+        f[3][ph] = cc;
+        f[4][ph] = comb3(__fsub_rn(ur, ul), an.dx[0], hmid, an.dx[1], __fsub_rn(dr, dl), an.dx[2]);
+        f[5][ph] = comb3(__fsub_rn(dl, ul), an.dy[0], vmid, an.dy[1], __fsub_rn(dr, ur), an.dy[2]);
+        f[6][ph] = comb3(__fsub_rn(dr, ul), an.d45[0], vmid, an.d45[1], hmid, an.d45[2]);
+        // (ur-dl)*a0 - vmid*a1 + hmid*a2, evaluated left to right
+        f[7][ph] = __fadd_rn(__fsub_rn(__fmul_rn(__fsub_rn(ur, dl), an.d135[0]), __fmul_rn(vmid, an.d135[1])),
+                             __fmul_rn(hmid, an.d135[2]));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        h8 v, r;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = f[2 * q + (e >> 2)][e & 3];
+          v[e] = (_Float16)x;
+          r[e] = (_Float16)(x - (float)v[e]);
+        }
+        *reinterpret_cast<h8*>(&feat[tid][8 * q]) = v;
+        if constexpr (PRECISE) *reinterpret_cast<h8*>(&feat[tid][32 + 8 * q]) = r;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const int p = wave * 64 + jg * 16 + n;          // pixel index inside the tile
+      const int ty = p / kPTW, tx = p - ty * kPTW;
+      const h8 bop = *reinterpret_cast<const h8*>(&feat[p][8 * g]);
+      f4 a0 = mfma_f16(A0, bop, f4{0.f, 0.f, 0.f, 0.f});
+      f4 a1 = mfma_f16(A1, bop, f4{0.f, 0.f, 0.f, 0.f});
+      if constexpr (PRECISE) {
+        const h8 blo = *reinterpret_cast<const h8*>(&feat[p][32 + 8 * g]);
+        a0 = mfma_f16(L0, bop, a0);
+        a1 = mfma_f16(L1, bop, a1);
+        a0 = mfma_f16(A0, blo, a0);
+        a1 = mfma_f16(A1, blo, a1);
+      }
+      const int qy = qy0 + ty, qx = qx0 + tx;
+      if (qy < Hq && qx < Wq) {
+        _Float16* dst = skip + (((size_t)b * Hq + qy) * Wq + qx) * 32 + 4 * g;
+        u2 w0, w1;
+        w0[0] = pack_h2(leaky(a0[0] + bs[0][0], 0.1f), leaky(a0[1] + bs[0][1], 0.1f));
+        w0[1] = pack_h2(leaky(a0[2] + bs[0][2], 0.1f), leaky(a0[3] + bs[0][3], 0.1f));
+        w1[0] = pack_h2(leaky(a1[0] + bs[1][0], 0.1f), leaky(a1[1] + bs[1][1], 0.1f));
+        w1[1] = pack_h2(leaky(a1[2] + bs[1][2], 0.1f), leaky(a1[3] + bs[1][3], 0.1f));
+        *reinterpret_cast<u2*>(dst) = w0;
+        *reinterpret_cast<u2*>(dst + 16) = w1;
+      }
+    }
+  }
+}
+
+int project_num_tiles(int batch, int Hq, int Wq) {
+  return batch * ((Hq + kPTH - 1) / kPTH) * ((Wq + kPTW - 1) / kPTW);
+}
+
+template <typename Tin, bool P>
+static void launch_project_t(const void* src, const void* wfrag, const float* bias, void* skip, const Analysis& an,
+                             int H, int W, int Hq, int Wq, int py, int px, int batch, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((project_kernel<Tin, P>), dim3(grid), dim3(256), 0, stream, (const Tin*)src, (const h8*)wfrag,
+                     bias, (_Float16*)skip, an, H, W, Hq, Wq, py, px, batch);
+}
+
+hipError_t launch_project(int in_fp32, int precise, const void* src, const void* wfrag, const float* bias, void* skip,
+                          const float* analysis24, int H, int W, int Hq, int Wq, int py, int px, int batch,
+                          int grid, hipStream_t stream) {
+  Analysis an;
+  const float* a = analysis24;
+  for (int i = 0; i < 9; ++i) an.basis[i] = a[i];
+  for (int i = 0; i < 3; ++i) {
+    an.mix[i] = a[9 + i]; an.dx[i] = a[12 + i]; an.dy[i] = a[15 + i];
+    an.d45[i] = a[18 + i]; an.d135[i] = a[21 + i];
+  }
+  if (in_fp32 && precise) launch_project_t<float, true>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);
+  else if (in_fp32) launch_project_t<float, false>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);
+  else if (precise) launch_project_t<_Float16, true>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);
+  else launch_project_t<_Float16, false>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);
+  return hipGetLastError();
+}
+
+int project_blocks_per_cu(int in_fp32, int precise) {
+  int n = 0;
+  hipError_t e;
+  if (in_fp32 && precise) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, project_kernel<float, true>, 256, 0);
+  else if (in_fp32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, project_kernel<float, false>, 256, 0);
+  else if (precise) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, project_kernel<_Float16, true>, 256, 0);
+  else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, project_kernel<_Float16, false>, 256, 0);
+  return e == hipSuccess && n > 0 ? n : 1;
+}
+
+}  // namespace aeisu

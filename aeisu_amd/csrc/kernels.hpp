@@ -1,0 +1,35 @@
+// Host-side launchers of the gfx950 kernels (defined in k_*.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace aeisu {
+
+int project_num_tiles(int batch, int Hq, int Wq);
+int grouped_num_tiles(int batch, int Hl, int Wl);
+int refine_num_tiles(int batch, int Hq, int Wq);
+int head_num_tiles(int batch, int H, int W);
+
+hipError_t launch_project(int in_fp32, int precise, const void* src, const void* wfrag, const float* bias, void* skip,
+                          const float* analysis24, int H, int W, int Hq, int Wq, int py, int px, int batch,
+                          int grid, hipStream_t stream);
+hipError_t launch_compress(int mode, const void* skip, const void* wfrag, const float* bias, const float* scale,
+                           void* low, float inv_in, float inv_out, int Hl, int Wl, int batch, int grid,
+                           hipStream_t stream);
+hipError_t launch_grouped(int mode, const void* in, const void* wfrag, const float* bias, const float* scale,
+                          void* out, float inv_out, int Hl, int Wl, int batch, int grid, hipStream_t stream);
+hipError_t launch_expand(int mode, const void* low, const void* skip, const void* wfrag, const float* bias,
+                         const float* scale, void* work, float inv_out, float s_out, int Hl, int Wl, int batch,
+                         int grid, hipStream_t stream);
+hipError_t launch_refine_tail(const void* work, const void* wfrag, const float* rbias, const float* tbias,
+                              void* meta, int Hq, int Wq, int batch, int grid, hipStream_t stream);
+hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* meta, const void* bankA,
+                       void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
+                       unsigned* nonfinite, int grid, hipStream_t stream);
+
+// Resident blocks per CU (occupancy), used to size the persistent grids.
+int head_blocks_per_cu(int in_fp32, int out_fp32);
+int project_blocks_per_cu(int in_fp32, int precise);
+int refine_blocks_per_cu();
+int body_blocks_per_cu(int kind, int mode);   // kind 0 compress, 1 grouped, 2 expand
+
+}  // namespace aeisu

@@ -1,0 +1,197 @@
+"""AEISU 2x upscaling throughput on one MI355X (BASELINE.json metric).
+
+Default workload = BASELINE config 2: 1920x1080 -> 3840x2160, batch 1, mixed
+FP8-E4M3 / FP16 (weights/aeisu_area_mixed_fp8.bin), FP16 frames in and out.
+A "step" is one frame through the whole path (controller + reconstruction
+head).  Frames are seeded synthetic scenes (aeisu_amd.frames), a pool of
+distinct frames resident in HBM before timing starts.
+
+Protocol:
+  1. W warm-up steps, then K timed steps replaying the per-frame HIP graph,
+     bracketed by torch.cuda.synchronize(): value = K / elapsed (frames/s).
+  2. K more steps launched eagerly with HIP events recorded on the launch
+     stream around every stage: per-kernel average durations -> roofline.
+  3. CPU baseline: the FP32 oracle restatement of the reference PyTorch path
+     (oracle/model.py, tile=0) on a bounded sample of the same frames.
+
+Prints ONE JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+MFMA_PEAK = {"fp16": 2.5e15, "fp8": 5.0e15, "int8": 5.0e15}
+CTRL_MAC_FP16 = 256 + 4608 + 1024        # project + refine + tail, per LR pixel (paper tex:352-359)
+CTRL_MAC_LOW = 512 + 4608 + 512          # compress + 4 bottlenecks + expand
+WORKLOADS = {
+    1: dict(precision="fp16", weights="aeisu_area.pt", name="aeisu_area fp16 1080p->4K b1"),
+    2: dict(precision="mixed", weights="aeisu_area_mixed_fp8.bin", name="aeisu_area mixed-fp8/fp16 1080p->4K b1"),
+    3: dict(precision="int8", weights="aeisu_int8_fp16.pt", name="aeisu int8/fp16 540p->1080p b8"),
+    4: dict(precision="mixed", weights="aeisu_div2k_l1_mixed_fp8.bin", name="aeisu_div2k_l1 mixed 1440p->5K b4"),
+}
+
+
+def geometry(h, w):
+    ey, ex = -h % 32, -w % 32
+    return h + 32 + ey, w + 32 + ex
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(frames_cpu, budget_s: float):
+    """FP32 oracle (reference PyTorch path restated) on whole frames until ~budget_s of work."""
+    import torch
+    from oracle import model as M
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    torch.set_num_threads(threads)
+    state = M.load_folded(ROOT / "weights" / "aeisu_area.pt")
+    f0 = frames_cpu[0].float()
+    M.upscale(state, f0[:, :256, :256], 0)                 # warm-up on a small crop
+    done, t0 = 0, time.perf_counter()
+    while True:
+        M.upscale(state, frames_cpu[done % len(frames_cpu)].float(), 0)
+        done += 1
+        if time.perf_counter() - t0 >= budget_s or done >= 8:
+            break
+    elapsed = time.perf_counter() - t0
+    return {"value": done / elapsed, "unit": "frames/s", "cores": threads, "kind": "port",
+            "ms_per_frame": 1000 * elapsed / done,
+            "sample": f"{done} whole {frames_cpu.shape[-2]}x{frames_cpu.shape[-1]} frame(s) through "
+                      f"oracle/model.py FP32 upscale(tile=0) (torch CPU, {threads} threads, "
+                      f"{platform.processor() or platform.machine()})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
+    ap.add_argument("--pool", type=int, default=4, help="distinct resident frames cycled through")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline work (0 = skip)")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replays")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
+              "(frames shard across GPUs with no exchange, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from aeisu_amd import frames as FR
+    from aeisu_amd import runtime as R
+    from aeisu_amd import _lib as L
+
+    wl = WORKLOADS[args.config]
+    spec = FR.CONFIGS[args.config]
+    B, H, W = spec["batch"], spec["height"], spec["width"]
+    dev = torch.device("cuda", 0)
+    log(f"bench: config {args.config} ({wl['name']}), generating {args.pool} frame batches")
+    pool_cpu = [FR.config_frames(args.config, seed=1000 * i) for i in range(args.pool)]
+    pool = [p.to(dev).contiguous() for p in pool_cpu]
+    outs = [torch.empty(B, 3, 2 * H, 2 * W, dtype=torch.float16, device=dev) for _ in pool]
+    model = R.load_model(ROOT / "weights" / wl["weights"], precision=wl["precision"])
+    stream = torch.cuda.current_stream()
+
+    def step(i, graph):
+        j = i % len(pool)
+        model.run(pool[j], out=outs[j], graph=graph, check_finite=False)
+
+    # --- 1. timed region: graph replays (or eager) --------------------------------------------------
+    graph = not args.eager
+    for i in range(args.warmup):
+        step(i, graph)
+    model.run(pool[0], out=outs[0])                          # finite check once, outside timing
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, graph)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1000 * elapsed / args.steps
+    log(f"bench: {ms_per_step:.4f} ms/step ({'graph' if graph else 'eager'})")
+
+    # --- 2. per-kernel HIP events on the launch stream ---------------------------------------------
+    hd = model.handle(B, H, W, torch.float16, torch.float16, L.FLAG_STAGE_TIMING)
+    for i in range(min(args.warmup, 5)):
+        L.check(L.lib().aeisu_upscale_async(hd.ptr, pool[i % len(pool)].data_ptr(), outs[i % len(pool)].data_ptr(),
+                                            stream.cuda_stream))
+    model.stage_timings(hd, reset=True)
+    t1 = time.perf_counter()
+    for i in range(args.steps):
+        j = i % len(pool)
+        L.check(L.lib().aeisu_upscale_async(hd.ptr, pool[j].data_ptr(), outs[j].data_ptr(), stream.cuda_stream))
+    torch.cuda.synchronize()
+    eager_ms = 1000 * (time.perf_counter() - t1) / args.steps
+    stages, nframes = model.stage_timings(hd, reset=True)
+    log("bench: stage ms " + ", ".join(f"{k}={v:.4f}" for k, v in stages.items()))
+
+    # --- algorithmic work per step -------------------------------------------------------------------
+    Hp, Wp = geometry(H, W)
+    lr_px = B * H * W
+    packed_px = B * (Hp // 2) * (Wp // 2)
+    s_io = 2                                                  # FP16 frames in and out
+    head_bytes = lr_px * (3 * s_io + 16 * 2 + 12 * s_io)      # RGB in + FP16 coefficients + 2x RGB out
+    refine_bytes = packed_px * (32 * 2 + 64 * 2)              # FP16 refine input + FP16 coefficient output
+    refine_flops = 2.0 * packed_px * (32 * 64 * 9 + 64 * 64)
+    low_kind = {"fp16": "fp16", "mixed": "fp8", "int8": "int8"}[wl["precision"]]
+    ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
+    ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
+    ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK["fp16"] + ctrl_flops_low / MFMA_PEAK[low_kind]
+    ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand", "refine_tail"))
+    head_s = stages["head"] / 1000
+    refine_s = stages["refine_tail"] / 1000
+    kernels = {
+        "head": {"bound": "hbm", "achieved": head_bytes / head_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                 "frac": head_bytes / head_s / HBM_PEAK, "ms": stages["head"],
+                 "algorithmic_bytes": head_bytes, "traffic": None},
+        "refine_tail": {"bound": "mfma", "achieved": refine_flops / refine_s / 1e12,
+                        "peak": MFMA_PEAK["fp16"] / 1e12, "unit": "TFLOP/s",
+                        "frac": refine_flops / refine_s / MFMA_PEAK["fp16"], "ms": stages["refine_tail"],
+                        "algorithmic_flops": refine_flops, "traffic": None},
+    }
+    dominant = max(kernels, key=lambda k: kernels[k]["ms"])
+    roof = {k: v for k, v in kernels[dominant].items() if k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+    roof["kernel"] = dominant
+
+    cpu = None
+    if args.cpu_budget > 0:
+        log("bench: CPU baseline")
+        cpu = cpu_baseline(torch.cat(pool_cpu)[:2], args.cpu_budget)
+
+    fps = B * 1000.0 / ms_per_step
+    line = {
+        "metric": "frames/s (ms/frame) 1080p->4K batch-1 mixed FP8/FP16; % MFMA / HBM roofline",
+        "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "ms_per_frame": round(ms_per_step / B, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": {"fp16": "fp16", "mixed": "fp8-e4m3/fp16", "int8": "int8/fp16"}[wl["precision"]],
+        "data": f"synthetic (aeisu_amd.frames config {args.config}, {args.pool} resident frames)",
+        "config": {"workload": wl["name"], "config_id": args.config, "batch": B, "input": [3, H, W],
+                   "output": [3, 2 * H, 2 * W], "precision": wl["precision"], "weights": wl["weights"],
+                   "timed": "graph replay" if graph else "eager"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "stages_ms": {k: round(v, 5) for k, v in stages.items()},
+        "eager_ms_per_step": round(eager_ms, 5),
+        "controller": {"ms": round(ctrl_ms, 5), "algorithmic_gflop": round((ctrl_flops16 + ctrl_flops_low) / 1e9, 3),
+                       "mfma_frac": ctrl_ideal_s / (ctrl_ms / 1000), "ideal_ms_at_mfma_peak": ctrl_ideal_s * 1000},
+        "timing_frames": nframes,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -3,9 +3,12 @@
 Three arithmetic policies, each a CPU restatement (torch float32/float64 plus
 the exact number-format rounding of ``oracle.quant``):
 
-* ``fp16``  -- every controller activation stored in FP16, FP32 accumulation,
-  FP32 head math on FP16 coefficients.  (Reference FP16 native route:
-  SrcPyrCudaRuntime.cu:4131-4873 with the cuDNN/WMMA FP16 stages.)
+* ``fp16``  -- every controller activation stored in FP16, FP16 weights, FP32
+  accumulation, FP32 head math on FP16 coefficients; the analysis features
+  and the project GEMM stay FP32-accurate (the project weights reach |w|~31
+  and FP16 operands there alone cost ~4e-3 of output error).  (Reference FP16
+  native route: SrcPyrCudaRuntime.cu:4131-4873 with the cuDNN/WMMA FP16 stages,
+  which rounds features and project weights to FP16.)
 * ``mixed`` -- the reference "Mixed" deployment: FP16 project/refine/tail,
   FP8-E4M3 compress, 4 grouped bottlenecks and expand with per-channel
   weight scales and per-tensor activation scales.  Quantization points follow
@@ -67,6 +70,7 @@ def weights_from_folded(state: Mapping[str, torch.Tensor]) -> Dict[str, object]:
         a, b = f"bottleneck_270_a{i + 1}", f"bottleneck_270_b{i + 1}"
         w[f"bottleneck{i}.w"] = f16(torch.cat((state[a + ".weight"], state[b + ".weight"])))
         w[f"bottleneck{i}.b"] = torch.cat((state[a + ".bias"], state[b + ".bias"])).float()
+    w["project.w32"] = state["project_540.weight"].float()
     w["base"], w["basis"] = state["base"].float(), state["basis"].float()
     return w
 
@@ -98,7 +102,7 @@ def weights_from_int8(record) -> Dict[str, object]:
         w[layer + ".wq"] = record["int8_weights"][layer].float()
         w[layer + ".factor"] = record["int8_factors"][layer].float()
         w[layer + ".b"] = record["int8_biases"][layer].float()
-    w["act"] = record["activation_scales"].float()
+    w["act"] = torch.as_tensor(record["activation_scales"], dtype=torch.float32)
     w["base"], w["basis"] = record["base"].float(), record["bank"].float()
     return w
 
@@ -151,8 +155,15 @@ def controller(src: torch.Tensor, w: Mapping[str, object], precision: str,
     GPU configs).  ``record`` (optional) receives the intermediate tensors.
     """
     rec = record if record is not None else {}
-    feat = features(src, w)
-    skip = project(feat, w)
+    if precision == "fp16":
+        # FP16 policy: the project GEMM runs on FP32-accurate operands (features and weights
+        # split into FP16 hi + lo on the GPU); its output is stored in FP16 like every activation.
+        feat = F.pixel_unshuffle(M.rgb_to_feature8(src, w), 2)
+        wp = w.get("project.w32", w["project.w"])
+        skip = f16(M.leaky(_conv64(feat, wp) + _chan(w["project.b"])))
+    else:
+        feat = features(src, w)
+        skip = project(feat, w)
     rec["features"], rec["skip"] = feat, skip
     act = w.get("act")
     if precision == "fp16":
