@@ -71,6 +71,23 @@ __device__ __forceinline__ float e4m3_to_f32(unsigned w) {
   return __builtin_amdgcn_cvt_f32_fp8((int)w, SEL);
 }
 
+// Eight E4M3 codes (bytes of w[0], w[1]) -> eight FP16 values.  Every E4M3 value is exactly
+// representable in FP16 (3-bit mantissa, exponents 2^-9 .. 2^8), so the conversion is exact.
+__device__ __forceinline__ h8 e4m3x8_to_h8(unsigned w0, unsigned w1) {
+  h8 r;
+  const unsigned w[2] = {w0, w1};
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[q], true);
+    r[4 * q + 0] = (_Float16)lo[0];
+    r[4 * q + 1] = (_Float16)lo[1];
+    r[4 * q + 2] = (_Float16)hi[0];
+    r[4 * q + 3] = (_Float16)hi[1];
+  }
+  return r;
+}
+
 // Symmetric INT8: clamp(rint(v * inv), -127, 127)  (rint = round half to even).
 __device__ __forceinline__ int quant_s8(float v, float inv) {
   float q = __builtin_rintf(v * inv);

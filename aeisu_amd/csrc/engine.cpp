@@ -195,6 +195,14 @@ static float f16_bits_to_f32(uint16_t b) {
   return (float)h;
 }
 
+// Value of an OCP E4M3 code (bias 7, 3 mantissa bits, subnormals below 2^-6; 0x7F/0xFF are NaN).
+static float e4m3_value(uint8_t code) {
+  const int e = (code >> 3) & 15, m = code & 7;
+  if (e == 15 && m == 7) return NAN;
+  const float v = e == 0 ? std::ldexp(float(m), -9) : std::ldexp(1.0f + m / 8.0f, e - 7);
+  return (code & 0x80) ? -v : v;
+}
+
 // out[(f*64 + lane)*E + i] = fn(f, m = lane & 15, slot = (lane >> 4)*E + i)
 template <typename T, typename Fn>
 static std::vector<T> pack_frags(int nfrag, int E, Fn fn) {
@@ -396,8 +404,8 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
     LayerDev& dst = li == 0 ? rt.compress : (li == 5 ? rt.expand : rt.grouped[li - 1]);
     require_prelu(a, l, cout, 0.1f);
     // generic element fetch W[o][i][tap] from whichever storage the policy uses
-    if (rt.mode == 0 || rt.mode == 1) {
-      const bool fp8 = rt.mode == 1;
+    if (rt.mode != 2) {
+      const bool fp8 = rt.mode == 1 || rt.mode == 3;
       const uint8_t* codes = fp8 ? a.need(l + ".weight_fp8", kE4M3, {cout, cin, ks, ks}).data : nullptr;
       const uint16_t* half = fp8 ? nullptr : a.need(l + ".weight_fp16", kF16, {cout, cin, ks, ks}).f16();
       auto W = [&](int o, int i, int tap) -> uint32_t {
@@ -422,8 +430,14 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
           return W(32 * (gt / 2) + 16 * (gt % 2) + m, s, tap);
         };
       }
-      if (fp8) dst.frag.upload(pack_frags<uint8_t>(nfrag, 8, [&](int f, int m, int s) { return (uint8_t)fn(f, m, s); }));
-      else dst.frag.upload(pack_frags<uint16_t>(nfrag, 8, [&](int f, int m, int s) { return (uint16_t)fn(f, m, s); }));
+      if (rt.mode == 1)
+        dst.frag.upload(pack_frags<uint8_t>(nfrag, 8, [&](int f, int m, int s) { return (uint8_t)fn(f, m, s); }));
+      else if (rt.mode == 3)  // E4M3 values widened exactly to FP16 for the FP16 MFMA
+        dst.frag.upload(pack_frags<uint16_t>(nfrag, 8, [&](int f, int m, int s) {
+          return f32_to_f16_bits(e4m3_value((uint8_t)fn(f, m, s)));
+        }));
+      else
+        dst.frag.upload(pack_frags<uint16_t>(nfrag, 8, [&](int f, int m, int s) { return (uint16_t)fn(f, m, s); }));
       if (fp8) {
         const int s_in = li == 0 ? 1 : li + 1;  // compress s1, bottleneck i s(i+2), expand s6
         const TensorView& ws = a.need(l + ".weight_scale", kF32, {cout});
@@ -654,11 +668,15 @@ static int create_impl(const uint8_t* data, size_t size, int precision, aeisu_ru
     if (!out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output handle");
     *out = nullptr;
     if (!data || size == 0) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "empty artifact");
-    if (precision != AEISU_PRECISION_FP16 && precision != AEISU_PRECISION_MIXED && precision != AEISU_PRECISION_INT8)
+    if (precision != AEISU_PRECISION_FP16 && precision != AEISU_PRECISION_MIXED &&
+        precision != AEISU_PRECISION_INT8 && precision != AEISU_PRECISION_MIXED_FP8MMA)
       aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "unknown precision");
     auto rt = std::make_unique<Runtime>();
     rt->precision = precision;
-    rt->mode = precision == AEISU_PRECISION_FP16 ? 0 : (precision == AEISU_PRECISION_MIXED ? 1 : 2);
+    // kernel modes: 0 FP16, 1 E4M3 on the FP8 MFMA, 2 INT8, 3 E4M3 values on the FP16 MFMA
+    rt->mode = precision == AEISU_PRECISION_FP16 ? 0
+               : precision == AEISU_PRECISION_MIXED ? 3
+               : precision == AEISU_PRECISION_MIXED_FP8MMA ? 1 : 2;
     {
       // host-only: parse, validate and pack every tensor before touching the device
       aeisu::Artifact art = aeisu::parse_artifact(data, size);

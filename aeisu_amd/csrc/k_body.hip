@@ -88,12 +88,15 @@ __global__ __launch_bounds__(256) void compress_kernel(
         }
       }
     }
-  } else if constexpr (MODE == 1) {
-    long A[4][4];
+  } else if constexpr (MODE == 1 || MODE == 3) {
+    // MODE 1: E4M3 operands on the FP8 MFMA.  MODE 3: the same E4M3 values widened
+    // (exactly) to FP16 for the FP16 MFMA, whose FP32 accumulation is exact per product.
+    typedef typename std::conditional<MODE == 1, long, h8>::type Frag;
+    Frag A[4][4];
 #pragma unroll
     for (int T = 0; T < 4; ++T)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) A[T][k] = reinterpret_cast<const long*>(wfrag)[(T * 4 + k) * 64 + lane];
+      for (int k = 0; k < 4; ++k) A[T][k] = reinterpret_cast<const Frag*>(wfrag)[(T * 4 + k) * 64 + lane];
     for (int G = blockIdx.x * 4 + wave; G < num_groups; G += gridDim.x * 4) {
       const int b = G / (Hl * gx), rem = G - b * Hl * gx, ly = rem / gx, lx = (rem - ly * gx) * 16 + n;
       const int lxc = min(lx, Wl - 1);
@@ -106,9 +109,15 @@ __global__ __launch_bounds__(256) void compress_kernel(
                                         h2f_lo(raw[1]) * inv_in, h2f_hi(raw[1]) * inv_in);
         const unsigned hi = pack_e4m3x4(h2f_lo(raw[2]) * inv_in, h2f_hi(raw[2]) * inv_in,
                                         h2f_lo(raw[3]) * inv_in, h2f_hi(raw[3]) * inv_in);
-        const long bop = (long)(((unsigned long)hi << 32) | lo);
+        if constexpr (MODE == 1) {
+          const long bop = (long)(((unsigned long)hi << 32) | lo);
 #pragma unroll
-        for (int T = 0; T < 4; ++T) acc[T] = mfma_fp8(A[T][k], bop, acc[T]);
+          for (int T = 0; T < 4; ++T) acc[T] = mfma_fp8(A[T][k], bop, acc[T]);
+        } else {
+          const h8 bop = e4m3x8_to_h8(lo, hi);
+#pragma unroll
+          for (int T = 0; T < 4; ++T) acc[T] = mfma_f16(A[T][k], bop, acc[T]);
+        }
       }
       if (lx < Wl) {
         unsigned char* dst = reinterpret_cast<unsigned char*>(low) + (((size_t)b * Hl + ly) * Wl + lx) * 64 + 4 * g;
@@ -168,8 +177,9 @@ template <int MODE>
 __global__ __launch_bounds__(256) void grouped_kernel(
     const void* __restrict__ in, const void* __restrict__ wfrag, const float* __restrict__ bias,
     const float* __restrict__ scale, void* __restrict__ out, float inv_out, int Hl, int Wl, int batch) {
-  constexpr int ES = MODE == 0 ? 2 : 1;                  // element size
-  constexpr int PIX = MODE == 0 ? 144 : 80;              // LDS bytes per pixel (64 ch + pad)
+  constexpr int ES = MODE == 0 ? 2 : 1;                  // element size in HBM
+  constexpr bool H16 = MODE == 0 || MODE == 3;           // FP16 operands in LDS / on the MFMA
+  constexpr int PIX = H16 ? 144 : 80;                    // LDS bytes per pixel (64 ch + pad)
   __shared__ __attribute__((aligned(16))) unsigned char patch[kGPH * kGPW * PIX];
   const int lane = lane_id(), wave = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
   const int grp = wave & 1, rowbase = (wave >> 1) * 2;
@@ -183,7 +193,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(
       sc[T][r] = MODE == 0 ? 0.f : scale[c];
     }
   constexpr int NK = MODE == 2 ? 5 : 9;                  // K-chunks (taps; i8 packs 2 taps)
-  typedef typename std::conditional<MODE == 0, h8, typename std::conditional<MODE == 1, long, i4>::type>::type Frag;
+  typedef typename std::conditional<H16, h8, typename std::conditional<MODE == 1, long, i4>::type>::type Frag;
   Frag A[2][NK];
 #pragma unroll
   for (int T = 0; T < 2; ++T)
@@ -207,7 +217,12 @@ __global__ __launch_bounds__(256) void grouped_kernel(
       u4 v = {0u, 0u, 0u, 0u};
       if (gy >= 0 && gy < Hl && gx >= 0 && gx < Wl)
         v = *reinterpret_cast<const u4*>(src + ((size_t)gy * Wl + gx) * 64 * ES + 16 * ch);
-      *reinterpret_cast<u4*>(patch + pix * PIX + 16 * ch) = v;
+      if constexpr (MODE == 3) {   // 16 E4M3 codes -> 16 FP16 values (32 bytes of LDS)
+        *reinterpret_cast<h8*>(patch + pix * PIX + 32 * ch) = e4m3x8_to_h8(v[0], v[1]);
+        *reinterpret_cast<h8*>(patch + pix * PIX + 32 * ch + 16) = e4m3x8_to_h8(v[2], v[3]);
+      } else {
+        *reinterpret_cast<u4*>(patch + pix * PIX + 16 * ch) = v;
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -230,7 +245,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(
             for (int T = 0; T < 2; ++T) acc[T] = mfma_i8(A[T][k], bop, acc[T]);
           } else {
             const int p = (row + k / 3) * kGPW + 16 * j + n + k % 3;
-            if constexpr (MODE == 0) {
+            if constexpr (H16) {
               const h8 bop = *reinterpret_cast<const h8*>(patch + p * PIX + 2 * (32 * grp + 8 * g));
 #pragma unroll
               for (int T = 0; T < 2; ++T) acc[T] = mfma_f16(A[T][k], bop, acc[T]);
@@ -251,7 +266,7 @@ __global__ __launch_bounds__(256) void grouped_kernel(
               w[0] = pack_h2(leaky(acc[T][0] + bs[T][0], 0.1f), leaky(acc[T][1] + bs[T][1], 0.1f));
               w[1] = pack_h2(leaky(acc[T][2] + bs[T][2], 0.1f), leaky(acc[T][3] + bs[T][3], 0.1f));
               *reinterpret_cast<u2*>(reinterpret_cast<_Float16*>(out) + pix * 64 + c0) = w;
-            } else if constexpr (MODE == 1) {
+            } else if constexpr (MODE == 1 || MODE == 3) {
               float v[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) v[r] = leaky(fmaf(acc[T][r], sc[T][r], bs[T][r]), 0.1f) * inv_out;
@@ -293,7 +308,8 @@ __global__ __launch_bounds__(256) void expand_kernel(
       sc[T][r] = MODE == 0 ? 0.f : scale[o];
     }
   constexpr int NK = MODE == 2 ? 1 : 2;
-  typedef typename std::conditional<MODE == 0, h8, typename std::conditional<MODE == 1, long, i4>::type>::type Frag;
+  typedef typename std::conditional<MODE == 0 || MODE == 3, h8,
+                                    typename std::conditional<MODE == 1, long, i4>::type>::type Frag;
   Frag A[8][NK];
 #pragma unroll
   for (int T = 0; T < 8; ++T)
@@ -319,6 +335,14 @@ __global__ __launch_bounds__(256) void expand_kernel(
 #pragma unroll
         for (int T = 0; T < 8; ++T) acc[T] = mfma_fp8(A[T][k], bop, acc[T]);
       }
+    } else if constexpr (MODE == 3) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const u2 raw = *reinterpret_cast<const u2*>(reinterpret_cast<const unsigned char*>(low) + pix * 64 + 32 * k + 8 * g);
+        const h8 bop = e4m3x8_to_h8(raw[0], raw[1]);
+#pragma unroll
+        for (int T = 0; T < 8; ++T) acc[T] = mfma_f16(A[T][k], bop, acc[T]);
+      }
     } else {
       const i4 bop = *reinterpret_cast<const i4*>(reinterpret_cast<const unsigned char*>(low) + pix * 64 + 16 * g);
 #pragma unroll
@@ -338,7 +362,7 @@ __global__ __launch_bounds__(256) void expand_kernel(
           const float e = (float)(_Float16)leaky(acc[T][r] + bs[T][r], 0.1f);
           v[r] = e + s[r];
         }
-      } else if constexpr (MODE == 1) {
+      } else if constexpr (MODE == 1 || MODE == 3) {
         const unsigned q = pack_e4m3x4(leaky(fmaf(acc[T][0], sc[T][0], bs[T][0]), 0.1f) * inv_out,
                                        leaky(fmaf(acc[T][1], sc[T][1], bs[T][1]), 0.1f) * inv_out,
                                        leaky(fmaf(acc[T][2], sc[T][2], bs[T][2]), 0.1f) * inv_out,
@@ -373,7 +397,12 @@ hipError_t launch_compress(int mode, const void* skip, const void* wfrag, const 
 #define AEISU_COMPRESS(M)                                                                                \
   hipLaunchKernelGGL(compress_kernel<M>, dim3(grid), dim3(256), 0, stream, (const _Float16*)skip, wfrag, \
                      bias, scale, low, inv_in, inv_out, Hl, Wl, batch)
-  if (mode == 0) AEISU_COMPRESS(0); else if (mode == 1) AEISU_COMPRESS(1); else AEISU_COMPRESS(2);
+  switch (mode) {
+    case 0: AEISU_COMPRESS(0); break;
+    case 1: AEISU_COMPRESS(1); break;
+    case 2: AEISU_COMPRESS(2); break;
+    default: AEISU_COMPRESS(3); break;
+  }
 #undef AEISU_COMPRESS
   return hipGetLastError();
 }
@@ -383,7 +412,12 @@ hipError_t launch_grouped(int mode, const void* in, const void* wfrag, const flo
 #define AEISU_GROUPED(M)                                                                                     \
   hipLaunchKernelGGL(grouped_kernel<M>, dim3(grid), dim3(256), 0, stream, in, wfrag, bias, scale, out, inv_out, \
                      Hl, Wl, batch)
-  if (mode == 0) AEISU_GROUPED(0); else if (mode == 1) AEISU_GROUPED(1); else AEISU_GROUPED(2);
+  switch (mode) {
+    case 0: AEISU_GROUPED(0); break;
+    case 1: AEISU_GROUPED(1); break;
+    case 2: AEISU_GROUPED(2); break;
+    default: AEISU_GROUPED(3); break;
+  }
 #undef AEISU_GROUPED
   return hipGetLastError();
 }
@@ -394,7 +428,12 @@ hipError_t launch_expand(int mode, const void* low, const void* skip, const void
 #define AEISU_EXPAND(M)                                                                                    \
   hipLaunchKernelGGL(expand_kernel<M>, dim3(grid), dim3(256), 0, stream, low, (const _Float16*)skip, wfrag, \
                      bias, scale, (_Float16*)work, inv_out, s_out, Hl, Wl, batch)
-  if (mode == 0) AEISU_EXPAND(0); else if (mode == 1) AEISU_EXPAND(1); else AEISU_EXPAND(2);
+  switch (mode) {
+    case 0: AEISU_EXPAND(0); break;
+    case 1: AEISU_EXPAND(1); break;
+    case 2: AEISU_EXPAND(2); break;
+    default: AEISU_EXPAND(3); break;
+  }
 #undef AEISU_EXPAND
   return hipGetLastError();
 }
@@ -402,10 +441,11 @@ hipError_t launch_expand(int mode, const void* low, const void* skip, const void
 int body_blocks_per_cu(int kind, int mode) {
   int n = 0;
   hipError_t e = hipErrorInvalidValue;
-#define AEISU_OCC(K) \
-  (mode == 0 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<0>, 256, 0) \
-   : mode == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<1>, 256, 0) \
-               : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<2>, 256, 0))
+#define AEISU_OCC(K)                                                                  \
+  (mode == 0   ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<0>, 256, 0)       \
+   : mode == 1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<1>, 256, 0)       \
+   : mode == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<2>, 256, 0)       \
+               : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K<3>, 256, 0))
   if (kind == 0) e = AEISU_OCC(compress_kernel);
   else if (kind == 1) e = AEISU_OCC(grouped_kernel);
   else e = AEISU_OCC(expand_kernel);

@@ -186,7 +186,7 @@ def load_model(path, device: str = "cuda", precision: Optional[str] = None) -> U
     """
     blob, natural = load_blob(Path(path))
     precision = precision or natural
-    allowed = {"fp16": {"fp16"}, "mixed": {"mixed", "fp16"}, "int8": {"int8"}}[natural]
+    allowed = {"fp16": {"fp16"}, "mixed": {"mixed", "mixed-fp8mma", "fp16"}, "int8": {"int8"}}[natural]
     if precision not in allowed:
         raise ValueError(f"{Path(path).name} provides {sorted(allowed)}, not {precision!r}")
     return Upscaler(blob, precision, device)

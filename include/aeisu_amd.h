@@ -33,8 +33,12 @@ extern "C" {
 
 /* arithmetic policies (NeuralRuntimeTypes.h:13-21 RuntimePrecision {Fp16, Fp8, Mixed} plus the INT8 route) */
 #define AEISU_PRECISION_FP16 1  /* FP16 operands, FP32 accumulation everywhere */
-#define AEISU_PRECISION_MIXED 2 /* FP8 E4M3 compress/bottleneck/expand, FP16 project/refine/tail/head */
+#define AEISU_PRECISION_MIXED 2 /* FP8 E4M3 compress/bottleneck/expand, FP16 project/refine/tail/head;
+                                   E4M3 operands widened exactly to FP16 on the FP16 MFMA (exact products,
+                                   FP32 accumulation) */
 #define AEISU_PRECISION_INT8 3  /* INT8 compress/bottleneck/expand, FP16 project/refine/tail/head */
+#define AEISU_PRECISION_MIXED_FP8MMA 4 /* as MIXED, but E4M3 operands on the FP8 MFMA (higher MFMA rate,
+                                          accumulation rounded inside the unit) */
 
 /* frame buffer layouts: planar RGB, batch-major [B][3][H][W] */
 #define AEISU_LAYOUT_NCHW_F16 0
