@@ -41,6 +41,18 @@ WORKLOADS = {
 }
 
 
+def measured_traffic(config: int):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (config 2 only)."""
+    path = ROOT / "profiles" / "hbm_traffic_mixed_1080p_pmc.md"
+    out = {}
+    if config == 2 and path.exists():
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes "):
+                _, name, value = line.split()
+                out["head" if name.startswith("head") else "refine_tail" if name.startswith("refine") else name] = int(value)
+    return out
+
+
 def geometry(h, w):
     ey, ex = -h % 32, -w % 32
     return h + 32 + ey, w + 32 + ex
@@ -82,6 +94,8 @@ def main():
     ap.add_argument("--pool", type=int, default=4, help="distinct resident frames cycled through")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replays")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (reference point for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
@@ -161,9 +175,22 @@ def main():
                         "frac": refine_flops / refine_s / MFMA_PEAK["fp16"], "ms": stages["refine_tail"],
                         "algorithmic_flops": refine_flops, "traffic": None},
     }
+    traffic = measured_traffic(args.config)
+    for k in kernels:
+        kernels[k]["traffic"] = traffic.get(k)
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     roof = {k: v for k, v in kernels[dominant].items() if k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
     roof["kernel"] = dominant
+
+    if args.copy_calibration:
+        # a plain copy kernel of known size: reads and writes exactly MIB MiB each
+        n = args.copy_calibration * (1 << 20) // 4
+        src_buf = torch.ones(n, dtype=torch.float32, device=dev)
+        dst_buf = torch.empty_like(src_buf)
+        for _ in range(3):
+            dst_buf.copy_(src_buf)
+        torch.cuda.synchronize()
+        log(f"bench: copy calibration {args.copy_calibration} MiB x3 done")
 
     cpu = None
     if args.cpu_budget > 0:

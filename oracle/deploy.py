@@ -134,7 +134,7 @@ def project(feat: torch.Tensor, w) -> torch.Tensor:
 
 def _fp8_epilogue(acc, w, layer, s_in, s_out) -> torch.Tensor:
     """fmaf(acc, s_in*wscale, bias_fp8) -> leaky -> e4m3(v * 1/s_out)."""
-    scale = (torch.tensor(s_in, dtype=torch.float32) * w[layer + ".ws"].float())
+    scale = (torch.tensor(float(s_in), dtype=torch.float32) * w[layer + ".ws"].float())
     v = fmaf(acc, _chan(scale), _chan(w[layer + ".b8"]))
     v = torch.where(v < 0, v * _chan(w[layer + ".prelu"]), v)
     return e4m3_round_t(v * torch.tensor(_inv(s_out), dtype=torch.float32))

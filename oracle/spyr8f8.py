@@ -22,7 +22,8 @@ DESC_SIZE = 80
 CHECKSUM_OFFSET = 184
 _HEADER = struct.Struct("<8sIIII64s14I2f4Q32s")       # 216 bytes before the reserved tail
 _DESC = struct.Struct("<32sIII4IQQ4s")
-DTYPES = {1: np.uint8, 2: np.float16, 3: np.float32}    # 1 = e4m3fn codes
+DTYPES = {1: np.uint8, 2: np.float16, 3: np.float32,    # 1 = e4m3fn codes
+          6: np.int8}                                   # 6 = INT8 (this build's extension for the INT8 policy)
 LAYER_NAMES = ("project", "compress", "bottleneck0", "bottleneck1", "bottleneck2",
                "bottleneck3", "expand", "refine", "tail")
 
