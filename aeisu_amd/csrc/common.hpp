@@ -41,15 +41,18 @@ __device__ __forceinline__ i4 mfma_i8(i4 a, i4 b, i4 c) {
 }
 
 // Cross-row lane exchanges of CDNA4 (v_permlane32_swap: lanes 32-63 of x <-> lanes 0-31 of y;
-// v_permlane16_swap: odd 16-lane rows of x <-> even rows of y).  Written as inline asm on
-// purpose: with the ROCm 7.2 compiler, adding the two results of the
-// __builtin_amdgcn_permlane{16,32}_swap builtin is miscompiled into r[0] + r[0].
-__device__ __forceinline__ void permlane32_swap(float& x, float& y) {
-  asm volatile("v_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-}
-__device__ __forceinline__ void permlane16_swap(float& x, float& y) {
-  asm volatile("v_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-}
+// v_permlane16_swap: odd 16-lane rows of x <-> even rows of y).  Both registers are written.
+// Written as inline asm on purpose: with the ROCm 7.2 compiler the
+// __builtin_amdgcn_permlane{16,32}_swap builtin is treated as writing only its first result
+// (adding the two results is compiled into r[0] + r[0]).  Inline asm is opaque to the hazard
+// recognizer, so each swap carries the two wait states gfx950 needs between a VALU write of
+// either operand and the swap (without them the swap reads partially updated operands).
+#define AEISU_SWAP_ASM(op) asm volatile("s_nop 1\n\t" op " %0, %1" : "+v"(x), "+v"(y))
+__device__ __forceinline__ void permlane32_swap(float& x, float& y) { AEISU_SWAP_ASM("v_permlane32_swap_b32"); }
+__device__ __forceinline__ void permlane16_swap(float& x, float& y) { AEISU_SWAP_ASM("v_permlane16_swap_b32"); }
+__device__ __forceinline__ void permlane32_swap_u(unsigned& x, unsigned& y) { AEISU_SWAP_ASM("v_permlane32_swap_b32"); }
+__device__ __forceinline__ void permlane16_swap_u(unsigned& x, unsigned& y) { AEISU_SWAP_ASM("v_permlane16_swap_b32"); }
+#undef AEISU_SWAP_ASM
 
 // LeakyReLU as written by the reference epilogues: negative inputs scaled by the slope.
 __device__ __forceinline__ float leaky(float v, float slope) { return v < 0.0f ? v * slope : v; }

@@ -475,21 +475,44 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
     }
   }
 
-  // --- head bank: [K_hi | K_lo] and [K_hi | base_hi, base_lo] fragments, rows tap*4 + phase
+  // --- head bank: A1 = [K_hi | (0.05K)_hi] and A2 = [K_lo | (0.05K)_lo] fragments (against the
+  // kernel's B = [u ; w], clamp(a) = u + 0.05 w), followed by the learned base in accumulator
+  // layout.  Row m = 4g + i of tile t < 6 is (tap 4t + g, phase i); tile 6 row 4g is (tap 24,
+  // phase 2(g&1) + (g>>1)), the phase lane group g holds after the kernel's cross-lane
+  // reduction; the other rows of tile 6 are zero.
   {
     const float* K = basis.f32();  // [25][16][4]
     const float* B = base.f32();   // [25][4]
-    auto hi = [](float v) { return f32_to_f16_bits(v); };
-    auto lo = [](float v) { return f32_to_f16_bits(v - f16_bits_to_f32(f32_to_f16_bits(v))); };
-    rt.head.frag.upload(pack_frags<uint16_t>(14, 8, [&](int f, int m, int s) -> uint16_t {
-      const int t = f % 7, row = 16 * t + m, tap = row / 4, ph = row % 4;
-      if (tap >= 25) return 0;
-      if (f < 7) return s < 16 ? hi(K[(tap * 16 + s) * 4 + ph]) : lo(K[(tap * 16 + s - 16) * 4 + ph]);
-      if (s < 16) return hi(K[(tap * 16 + s) * 4 + ph]);
-      if (s == 16) return hi(B[tap * 4 + ph]);
-      if (s == 17) return lo(B[tap * 4 + ph]);
-      return 0;
-    }));
+    auto row_of = [](int t, int m, int& tap, int& ph) {
+      const int g = m / 4, i = m % 4;
+      tap = 4 * t + g;
+      ph = i;
+      if (t == 6) {
+        tap = i == 0 ? 24 : -1;
+        ph = ((g & 1) << 1) | (g >> 1);
+      }
+    };
+    auto split = [](double v, bool want_lo) {
+      const uint16_t h = f32_to_f16_bits((float)v);
+      return want_lo ? f32_to_f16_bits((float)(v - (double)f16_bits_to_f32(h))) : h;
+    };
+    std::vector<uint16_t> frags = pack_frags<uint16_t>(14, 8, [&](int f, int m, int s) -> uint16_t {
+      int tap, ph;
+      row_of(f % 7, m, tap, ph);
+      if (tap < 0) return 0;
+      const double k = K[(tap * 16 + (s & 15)) * 4 + ph];
+      return split(s < 16 ? k : 0.05 * k, f >= 7);
+    });
+    std::vector<uint8_t> img(frags.size() * 2 + 7 * 16 * sizeof(float));
+    std::memcpy(img.data(), frags.data(), frags.size() * 2);
+    float* bl = reinterpret_cast<float*>(img.data() + frags.size() * 2);
+    for (int t = 0; t < 7; ++t)
+      for (int m = 0; m < 16; ++m) {
+        int tap, ph;
+        row_of(t, m, tap, ph);
+        bl[t * 16 + m] = tap < 0 ? 0.f : B[tap * 4 + ph];
+      }
+    rt.head.frag.upload(img);
   }
 }
 

@@ -7,145 +7,250 @@
 //   W[t,ph] = base[t,ph] + sum_k a_k * bank[t,k,ph]                (t: 25 taps, ph: 4 phases)
 //   out[c, 2y + ph/2, 2x + ph%2] = clamp01( sum_t W[t,ph] * src[c, clamp(y+dy_t), clamp(x+dx_t)] )
 //
-// gfx950 mapping.  One wave handles 16 consecutive LR pixels of a row.
-//  * Synthesis on MFMA (16x16x32 f16): D[112 x 16] = Bank^T[112 x K] . Coef[K x 16],
-//    rows = tap*4 + phase (7 row tiles, taps 25..27 zero).  The FP32 bank is
-//    split into FP16 hi + lo halves; two MFMAs per row tile compute
-//      [K_hi | K_lo] . [a_hi ; a_hi]   and   [K_hi | base_hi, base_lo] . [a_lo ; 1, 1]
-//    giving W to ~2^-22 relative accuracy with the base folded in.  a_lo is
-//    non-zero only for clamped coefficients; the unclamped fast path feeds the
-//    raw FP16 coefficients straight into the MFMA.
-//  * Accumulator lane (n, g) holds W for pixel n, tap 4t+g, phases 0..3, so
-//    each lane applies 7 taps x 4 phases x 3 channels with FP32 FMAs from an
-//    LDS RGB tile; the four lane groups are summed with permlane32/16 swaps.
+// gfx950 mapping.  One wave handles 16 consecutive LR pixels of a row per chunk.
+//  * Clamp without FP32 arithmetic: with s = sign(v),
+//      clamp(v) = u + 0.05 w,   u = s min(|v|, 2),   w = s max(min(|v|, 12) - 2, 0),
+//    where u and w are exact FP16 values computed with packed FP16 / u16 operations
+//    (NaN coefficients keep a NaN u).  Lane (n, g) splits coefficients 4g..4g+3 of
+//    pixel n (each coefficient once per wave); two permlane swaps then give lane
+//    group g the MFMA operand slots 8g..8g+7 of B = [u(0..15) ; w(0..15)].
+//  * Synthesis on MFMA (16x16x32 f16): D[112 x 16] = Bank^T[112 x 32] . B[32 x 16], two
+//    MFMAs per row tile with FP32 accumulation, the learned base as the C operand:
+//      W = base + [K_hi | (0.05K)_hi] . B + [K_lo | (0.05K)_lo] . B
+//    (FP32 bank and 0.05 * bank split into FP16 hi + lo, ~2^-22 relative to the FP32 math).
+//  * Row layout (packed on the host): tiles 0..5, row 4g+i = (tap 4t+g, phase i);
+//    tile 6, row 4g = (tap 24, phase ph(g)), other rows zero.  Accumulator lane
+//    (n, g) therefore holds W for pixel n, taps 4t+g (t < 6), all four phases:
+//    it applies those 6 taps x 4 phases x 3 channels with FP32 FMAs from an LDS
+//    RGB tile, the four lane groups are summed with permlane32/16 swaps, after
+//    which lane group g holds phase ph(g) = 2(g&1) + (g>>1) and adds tap 24.
+//  * Pipelining: a block walks tiles of 64x4 LR pixels; the RGB tile (with a
+//    2-pixel clamped halo) and each lane's FP16 coefficients of the NEXT tile
+//    are loaded into registers while the current tile is computed, and the RGB
+//    tile is double-buffered in LDS (one barrier per tile).
+//  * Output: partner lanes (g, g+2) hold horizontally adjacent output pixels;
+//    one permlane32 swap pairs them, so each store writes two values.  A per-lane
+//    running sum 0 * output (NaN for any non-finite output) sets the nonfinite
+//    flag once per wave at the end.
 #include "common.hpp"
 
 namespace aeisu {
 
 constexpr int kHeadTW = 64, kHeadTH = 4;
 constexpr int kHeadLW = kHeadTW + 4, kHeadLH = kHeadTH + 4;
+constexpr int kHeadLPos = kHeadLW * kHeadLH;              // RGB positions per tile (with halo)
+constexpr int kHeadFill = (kHeadLPos + 255) / 256;        // positions loaded per thread
+constexpr int kHeadChunks = kHeadTW / 16;
+constexpr int kHeadFrags = 14;                            // 7 row tiles x {hi, lo} fragments
 
 template <typename Tin>
 __device__ __forceinline__ float load_px(const Tin* p) { return (float)*p; }
 
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+// 2 FP16 coefficients (one dword) -> (u, w) with clamp(v) = u + 0.05 w, both exact in FP16.
+__device__ __forceinline__ void clamp_split(unsigned v, unsigned& u, unsigned& w) {
+  const unsigned mag = v & 0x7FFF7FFFu;
+  const us2 m = __builtin_bit_cast(us2, mag);
+  const us2 nanpart = __builtin_elementwise_sub_sat(m, (us2){0x7C00, 0x7C00});  // > 0 only for NaN
+  const us2 mc = __builtin_elementwise_min(m, (us2){0x4A00, 0x4A00});           // min(|v|, 12.0)
+  const h2 mch = __builtin_bit_cast(h2, mc);
+  const h2 e = __builtin_elementwise_max(mch - (h2){2, 2}, (h2){0, 0});          // exact
+  const h2 um = mch - e;                                                          // min(|v|, 2), exact
+  unsigned nanbits;                                                               // 0, or NaN exponent+mantissa
+  asm("v_pk_mad_u16 %0, %1, %2, 0 clamp" : "=v"(nanbits) : "v"(__builtin_bit_cast(unsigned, nanpart)),
+      "s"(0x7E007E00u));
+  u = ((__builtin_bit_cast(unsigned, um) | nanbits) & 0x7FFF7FFFu) | (v & 0x80008000u);
+  w = (__builtin_bit_cast(unsigned, e) & 0x7FFF7FFFu) | (v & 0x80008000u);
+}
+
+struct HeadTile {
+  int b, y0, x0;
+};
+__device__ __forceinline__ HeadTile head_tile(int tidx, int tiles_x, int tiles_y) {
+  HeadTile t;
+  t.b = tidx / (tiles_y * tiles_x);
+  const int rem = tidx - t.b * tiles_y * tiles_x;
+  t.y0 = (rem / tiles_x) * kHeadTH;
+  t.x0 = (rem % tiles_x) * kHeadTW;
+  return t;
+}
+
+// Registers holding one tile's inputs ahead of its computation.
+struct HeadPrefetch {
+  float rgb[kHeadFill][3];   // this thread's share of the clamped RGB tile
+  u2 coef[kHeadChunks];      // this lane's 4 FP16 coefficients for each chunk of its row
+};
+
+template <typename Tin>
+__device__ __forceinline__ void head_fetch(HeadPrefetch& p, const Tin* __restrict__ src,
+                                           const _Float16* __restrict__ meta, HeadTile t, int H, int W,
+                                           int Hq, int Wq, int py, int px, int wave, int n, int g) {
+  const size_t plane = (size_t)H * W;
+  const Tin* s = src + (size_t)t.b * 3 * plane;
+#pragma unroll
+  for (int k = 0; k < kHeadFill; ++k) {
+    const int q = threadIdx.x + 256 * k;
+    if (q < kHeadLPos) {
+      const int ly = q / kHeadLW, lx = q - ly * kHeadLW;
+      const int sy = min(max(t.y0 + ly - 2, 0), H - 1), sx = min(max(t.x0 + lx - 2, 0), W - 1);
+      const size_t o = (size_t)sy * W + sx;
+      p.rgb[k][0] = load_px(s + o);
+      p.rgb[k][1] = load_px(s + plane + o);
+      p.rgb[k][2] = load_px(s + 2 * plane + o);
+    }
+  }
+  // Rows / columns past the frame edge are clamped so every load stays inside the tensor;
+  // the clamped chunks are never stored.
+  const int Y = min(t.y0 + wave, H - 1) + py;
+  const _Float16* mrow = meta + ((size_t)t.b * Hq + (Y >> 1)) * Wq * 64;
+#pragma unroll
+  for (int j = 0; j < kHeadChunks; ++j) {
+    const int X = min(t.x0 + 16 * j + n, W - 1) + px;
+    const int rho = ((Y & 1) << 1) | (X & 1);
+    p.coef[j] = *reinterpret_cast<const u2*>(mrow + (size_t)(X >> 1) * 64 + 16 * rho + 4 * g);
+  }
+}
+
+template <typename Tout>
+__device__ __forceinline__ void store_pair(Tout* p, float left, float right);
+template <>
+__device__ __forceinline__ void store_pair<_Float16>(_Float16* p, float left, float right) {
+  *reinterpret_cast<unsigned*>(p) = pack_h2(left, right);
+}
+template <>
+__device__ __forceinline__ void store_pair<float>(float* p, float left, float right) {
+  *reinterpret_cast<float2*>(p) = make_float2(left, right);
+}
+
 template <typename Tin, typename Tout>
-__global__ __launch_bounds__(256) void head_kernel(
+__global__ __launch_bounds__(256, 3) void head_kernel(
     const Tin* __restrict__ src, const _Float16* __restrict__ meta, const h8* __restrict__ bankA,
     Tout* __restrict__ out, int H, int W, int Hq, int Wq, int py, int px, int batch,
     unsigned* __restrict__ nonfinite) {
-  __shared__ float4 tile[kHeadLH][kHeadLW];
+  __shared__ float4 tiles[2][kHeadLPos];
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  h8 A1[7], A3[7];
+  h8 A1[7], A2[7];   // [K_hi | (0.05K)_hi] and [K_lo | (0.05K)_lo] fragments
+  f4 base[7];        // learned base in accumulator layout (rows 4g..4g+3 of each tile)
+  const f4* base_src = reinterpret_cast<const f4*>(bankA + kHeadFrags * 64);
 #pragma unroll
   for (int t = 0; t < 7; ++t) {
     A1[t] = bankA[t * 64 + lane];
-    A3[t] = bankA[(7 + t) * 64 + lane];
+    A2[t] = bankA[(7 + t) * 64 + lane];
+    base[t] = base_src[t * 4 + g];
   }
+  // LDS offsets (float4 units, relative to the pixel's top-left tap) of taps 4t+g
+  int toff[6];
+#pragma unroll
+  for (int t = 0; t < 6; ++t) {
+    const int tap = 4 * t + g;
+    toff[t] = (tap / 5) * kHeadLW + tap % 5;
+  }
+  float chk = 0.f;   // 0 * every output of this lane: NaN iff one was not finite
+
   const int tiles_x = (W + kHeadTW - 1) / kHeadTW, tiles_y = (H + kHeadTH - 1) / kHeadTH;
   const int num_tiles = batch * tiles_y * tiles_x;
   const int iters = tile_iters(num_tiles);
-  const size_t plane = (size_t)H * W, oplane = (size_t)4 * H * W;
-  // constant B operand of the base MFMA: slots 16, 17 = 1 (lane group 2, first two halves)
-  h8 bconst = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (g == 2) { bconst[0] = (_Float16)1.0f; bconst[1] = (_Float16)1.0f; }
+  const size_t oplane = (size_t)4 * H * W;
+
+  int tidx = tile_of(0, num_tiles);
+  HeadPrefetch cur;
+  if (tidx < num_tiles)
+    head_fetch(cur, src, meta, head_tile(tidx, tiles_x, tiles_y), H, W, Hq, Wq, py, px, wave, n, g);
 
   for (int it = 0; it < iters; ++it) {
-    const int tidx = tile_of(it, num_tiles);
     if (tidx >= num_tiles) break;                    // block-uniform
-    const int b = tidx / (tiles_y * tiles_x);
-    const int rem = tidx - b * tiles_y * tiles_x;
-    const int y0 = (rem / tiles_x) * kHeadTH, x0 = (rem % tiles_x) * kHeadTW;
-    const Tin* s = src + (size_t)b * 3 * plane;
-    __syncthreads();
-    for (int q = threadIdx.x; q < kHeadLH * kHeadLW; q += 256) {
-      const int ly = q / kHeadLW, lx = q - ly * kHeadLW;
-      const int sy = min(max(y0 + ly - 2, 0), H - 1), sx = min(max(x0 + lx - 2, 0), W - 1);
-      const size_t o = (size_t)sy * W + sx;
-      tile[ly][lx] = make_float4(load_px(s + o), load_px(s + plane + o), load_px(s + 2 * plane + o), 0.f);
+    const HeadTile t = head_tile(tidx, tiles_x, tiles_y);
+    float4* buf = tiles[it & 1];
+#pragma unroll
+    for (int k = 0; k < kHeadFill; ++k) {
+      const int q = threadIdx.x + 256 * k;
+      if (q < kHeadLPos) buf[q] = make_float4(cur.rgb[k][0], cur.rgb[k][1], cur.rgb[k][2], 0.f);
     }
-    __syncthreads();
-    const int y = y0 + wave;
-    if (y >= H) continue;                              // wave-uniform
-    const _Float16* mrow = meta + (size_t)b * Hq * Wq * 64;
-    Tout* ob = out + (size_t)b * 3 * oplane;
-#pragma unroll 1
-    for (int j = 0; j < kHeadTW / 16; ++j) {
-      const int x = x0 + 16 * j + n;
-      if (x0 + 16 * j >= W) break;                     // wave-uniform
-      const int xc = min(x, W - 1);
-      const int Y = y + py, X = xc + px;
-      const int rho = ((Y & 1) << 1) | (X & 1);
-      const u4 raw = *reinterpret_cast<const u4*>(mrow + ((size_t)(Y >> 1) * Wq + (X >> 1)) * 64 + 16 * rho + 8 * (g & 1));
-      unsigned big = 0;
+    const u2 coef[kHeadChunks] = {cur.coef[0], cur.coef[1], cur.coef[2], cur.coef[3]};
+    const int ntidx = tile_of(it + 1, num_tiles);
+    if (ntidx < num_tiles)
+      head_fetch(cur, src, meta, head_tile(ntidx, tiles_x, tiles_y), H, W, Hq, Wq, py, px, wave, n, g);
+    __syncthreads();                                 // buf complete; the other buffer is free again
+
+    const int y = t.y0 + wave;
+    if (y < H) {                                     // wave-uniform
+      Tout* ob = out + (size_t)t.b * 3 * oplane;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) big |= ((raw[w] & 0x7FFF7FFFu) + 0x3FFF3FFFu) & 0x80008000u;
-      h8 b1, b3;
-      if (__ballot(big != 0) == 0ull) {
-        b1 = __builtin_bit_cast(h8, raw);
-        b3 = bconst;
-      } else {
-        h8 hi, lo;
+      for (int j = 0; j < kHeadChunks; ++j) {
+        if (t.x0 + 16 * j >= W) break;               // wave-uniform
+        const int x = t.x0 + 16 * j + n;
+        // coefficients 4g..4g+3 of pixel n -> (u, w) halves, then regroup across lane groups
+        unsigned U[2], Wd[2];
+        clamp_split(coef[j][0], U[0], Wd[0]);
+        clamp_split(coef[j][1], U[1], Wd[1]);
+        // (U, W) of groups 0..3 -> group g holds slots 8g..8g+7 of [u ; w]
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const unsigned w = raw[i >> 1];
-          const float t = (i & 1) ? h2f_hi(w) : h2f_lo(w);
-          const float mag = fabsf(t);
-          float c = t;
-          if (mag > 2.0f) c = copysignf(fminf(2.5f, fmaf(0.05f, mag - 2.0f, 2.0f)), t);
-          hi[i] = (_Float16)c;
-          lo[i] = (_Float16)(c - (float)hi[i]);
+        for (int w = 0; w < 2; ++w) permlane32_swap_u(U[w], Wd[w]);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) permlane16_swap_u(U[w], Wd[w]);
+        const u4 bw = {U[0], U[1], Wd[0], Wd[1]};
+        const h8 bop = __builtin_bit_cast(h8, bw);
+        f4 acc[7];
+#pragma unroll
+        for (int r = 0; r < 7; ++r) {
+          acc[r] = mfma_f16(A1[r], bop, base[r]);
+          acc[r] = mfma_f16(A2[r], bop, acc[r]);
         }
-        b1 = hi;
-        b3 = (g < 2) ? lo : bconst;
-      }
-      f4 acc[7];
+        const float4* L0 = buf + wave * kHeadLW + 16 * j + n;
+        float o[12];
 #pragma unroll
-      for (int t = 0; t < 7; ++t) {
-        acc[t] = mfma_f16(A1[t], b1, f4{0.f, 0.f, 0.f, 0.f});
-        acc[t] = mfma_f16(A3[t], b3, acc[t]);
-      }
-      float o[12];
+        for (int i = 0; i < 12; ++i) o[i] = 0.f;
 #pragma unroll
-      for (int i = 0; i < 12; ++i) o[i] = 0.f;
+        for (int r = 0; r < 6; ++r) {
+          const float4 L = L0[toff[r]];
 #pragma unroll
-      for (int t = 0; t < 7; ++t) {
-        const int tap = min(4 * t + g, 24);            // taps >= 25 carry zero weights
-        const int dy = tap / 5, dx = tap - 5 * (tap / 5);
-        const float4 L = tile[wave + dy][16 * j + n + dx];
-#pragma unroll
-        for (int ph = 0; ph < 4; ++ph) {
-          o[0 * 4 + ph] = fmaf(acc[t][ph], L.x, o[0 * 4 + ph]);
-          o[1 * 4 + ph] = fmaf(acc[t][ph], L.y, o[1 * 4 + ph]);
-          o[2 * 4 + ph] = fmaf(acc[t][ph], L.z, o[2 * 4 + ph]);
+          for (int ph = 0; ph < 4; ++ph) {
+            o[0 * 4 + ph] = fmaf(acc[r][ph], L.x, o[0 * 4 + ph]);
+            o[1 * 4 + ph] = fmaf(acc[r][ph], L.y, o[1 * 4 + ph]);
+            o[2 * 4 + ph] = fmaf(acc[r][ph], L.z, o[2 * 4 + ph]);
+          }
         }
-      }
-      // Sum the four lane groups (g = lane >> 4) holding the same pixel.
-      float s[6];
+        // Sum the four lane groups (g = lane >> 4) holding the same pixel.
+        float s[6];
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        float x = o[2 * i], z = o[2 * i + 1];
-        permlane32_swap(x, z);
-        s[i] = x + z;
-      }
-      float u[3];
+        for (int i = 0; i < 6; ++i) {
+          float a = o[2 * i], z = o[2 * i + 1];
+          permlane32_swap(a, z);
+          s[i] = a + z;
+        }
+        float u[3];
 #pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        float x = s[2 * c], z = s[2 * c + 1];
-        permlane16_swap(x, z);
-        u[c] = x + z;
-      }
-      // lane row g now holds phase ph = ((g & 1) << 1) | (g >> 1) of pixel n, channels 0..2
-      const int ph = ((g & 1) << 1) | (g >> 1);
-      if (x < W) {
-        const bool bad = !(__builtin_isfinite(u[0]) && __builtin_isfinite(u[1]) && __builtin_isfinite(u[2]));
-        if (bad && nonfinite) atomicOr(nonfinite, 1u);
-        const size_t o_off = (size_t)(2 * y + (ph >> 1)) * (2 * W) + 2 * x + (ph & 1);
+        for (int c = 0; c < 3; ++c) {
+          float a = s[2 * c], z = s[2 * c + 1];
+          permlane16_swap(a, z);
+          u[c] = a + z;
+        }
+        // lane group g now holds phase ph(g) of pixel n; add tap 24 (dy = dx = 4)
+        const float4 L24 = L0[4 * kHeadLW + 4];
+        u[0] = fmaf(acc[6][0], L24.x, u[0]);
+        u[1] = fmaf(acc[6][0], L24.y, u[1]);
+        u[2] = fmaf(acc[6][0], L24.z, u[2]);
+        chk = fmaf(u[0] + u[1] + u[2], 0.0f, chk);
+        // pair phase ph(g) (left column) with ph(g+2) = ph(g) + 1 (right column) in lanes 0..31
+        float left[3], right[3];
 #pragma unroll
-        for (int c = 0; c < 3; ++c) ob[c * oplane + o_off] = (Tout)__builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f);
+        for (int c = 0; c < 3; ++c) {
+          left[c] = __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f);
+          right[c] = left[c];
+          permlane32_swap(left[c], right[c]);
+        }
+        if (g < 2 && x < W) {
+          Tout* p = ob + (size_t)(2 * y + g) * (2 * W) + 2 * x;
+#pragma unroll
+          for (int c = 0; c < 3; ++c) store_pair<Tout>(p + c * oplane, left[c], right[c]);
+        }
       }
     }
+    tidx = ntidx;
   }
+  if (nonfinite && __ballot(chk != chk) != 0ull && lane == 0) atomicOr(nonfinite, 1u);
 }
 
 template <typename Tin, typename Tout>
