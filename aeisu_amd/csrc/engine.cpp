@@ -276,7 +276,9 @@ struct Runtime {
   DeviceBuffer skip, work, meta, nonfinite;
   DeviceBuffer low[5];
   int nlow = 2;
-  struct Grids { int project, compress, grouped, expand, refine, head; } grid{};
+  bool fused = false;              // refine + tail + head in one kernel (coefficients on chip)
+  bool fused_ready = false;        // fused kernels' LDS limit raised on this device
+  struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
   // captured frame graphs, one per (input, output) buffer pair (a small LRU-free cache)
   struct Graph {
     const void* in;
@@ -538,7 +540,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   if ((in_layout != AEISU_LAYOUT_NCHW_F16 && in_layout != AEISU_LAYOUT_NCHW_F32) ||
       (out_layout != AEISU_LAYOUT_NCHW_F16 && out_layout != AEISU_LAYOUT_NCHW_F32))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unsupported frame layout");
-  if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD))
+  if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD | AEISU_FLAG_UNFUSED))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unknown configure flag");
   const bool no_pad = flags & AEISU_FLAG_NO_PAD;
   if (no_pad && (height % 4 || width % 4))
@@ -571,7 +573,9 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   const size_t packed = size_t(batch) * rt.Hq * rt.Wq, lowpx = size_t(batch) * rt.Hl * rt.Wl;
   rt.skip.alloc(packed * 32 * 2);
   rt.work.alloc(packed * 32 * 2);
-  rt.meta.alloc(packed * 64 * 2);
+  // the coefficient tensor only exists in device memory on the unfused path
+  if (flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED)) rt.meta.alloc(packed * 64 * 2);
+  else rt.meta.release();
   rt.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : 2;
   for (int i = 0; i < 5; ++i) {
     if (i < rt.nlow) rt.low[i].alloc(lowpx * 64 * rt.low_elem());
@@ -587,6 +591,12 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, m), cus);
   rt.grid.refine = clamp_grid(refine_num_tiles(batch, rt.Hq, rt.Wq), refine_blocks_per_cu(), cus);
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
+  rt.fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
+  rt.grid.fused = clamp_grid(fused_num_tiles(batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
+  if (rt.fused && !rt.fused_ready) {
+    check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
+    rt.fused_ready = true;
+  }
   rt.configured = true;
 }
 
@@ -595,7 +605,8 @@ static float inv(float s) { return 1.0f / s; }
 // Low-buffer slot written by body layer li (0 compress, 1..4 bottlenecks).
 static int low_slot(const Runtime& rt, int li) { return rt.nlow == 5 ? li : (li % 2); }
 
-static void enqueue_controller(Runtime& rt, const void* d_in, void* d_meta, hipStream_t s, hipEvent_t* ev) {
+// project .. expand (the controller up to the FP16 work tensor); events 0..4
+static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_t* ev) {
   const int m = rt.mode;
   if (ev) check_hip(hipEventRecord(ev[0], s), "hipEventRecord");
   check_hip(launch_project(rt.in_fp32, rt.project_precise, d_in, rt.project.frag.ptr, rt.project.bias.as<float>(), rt.skip.ptr, rt.analysis,
@@ -616,6 +627,10 @@ static void enqueue_controller(Runtime& rt, const void* d_in, void* d_meta, hipS
                           rt.expand.scale.as<float>(), rt.work.ptr, m ? inv(A[7]) : 0.f, m ? A[7] : 0.f, rt.Hl, rt.Wl,
                           rt.batch, rt.grid.expand, s), "expand launch");
   if (ev) check_hip(hipEventRecord(ev[4], s), "hipEventRecord");
+}
+
+static void enqueue_controller(Runtime& rt, const void* d_in, void* d_meta, hipStream_t s, hipEvent_t* ev) {
+  enqueue_body(rt, d_in, s, ev);
   check_hip(launch_refine_tail(rt.work.ptr, rt.refine_tail.frag.ptr, rt.refine_tail.bias.as<float>(),
                                rt.tail_bias.as<float>(), d_meta, rt.Hq, rt.Wq, rt.batch, rt.grid.refine, s),
             "refine/tail launch");
@@ -639,8 +654,20 @@ static hipEvent_t* next_events(Runtime& rt) {
 }
 
 static void enqueue_frame(Runtime& rt, const void* d_in, void* d_out, hipStream_t s, hipEvent_t* ev) {
-  enqueue_controller(rt, d_in, rt.meta.ptr, s, ev);
-  enqueue_head(rt, d_in, rt.meta.ptr, d_out, s);
+  if (!rt.fused) {
+    enqueue_controller(rt, d_in, rt.meta.ptr, s, ev);
+    enqueue_head(rt, d_in, rt.meta.ptr, d_out, s);
+    if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
+    return;
+  }
+  // fused path: the refine_tail stage is empty, the head stage times the fused kernel
+  enqueue_body(rt, d_in, s, ev);
+  if (ev) check_hip(hipEventRecord(ev[5], s), "hipEventRecord");
+  check_hip(launch_fused_tail_head(rt.in_fp32, rt.out_fp32, rt.work.ptr, d_in, rt.refine_tail.frag.ptr,
+                                   rt.refine_tail.bias.as<float>(), rt.tail_bias.as<float>(), rt.head.frag.ptr, d_out,
+                                   rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.nonfinite.as<unsigned>(),
+                                   rt.grid.fused, s),
+            "fused refine/tail/head launch");
   if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
 }
 
@@ -850,8 +877,12 @@ int aeisu_copy_intermediate(aeisu_runtime* h, int which, void* d_dst, size_t byt
     const void* src = nullptr;
     if (which == AEISU_BUF_SKIP) src = rt.skip.ptr;
     else if (which == AEISU_BUF_WORK) src = rt.work.ptr;
-    else if (which == AEISU_BUF_META) src = rt.meta.ptr;
-    else {
+    else if (which == AEISU_BUF_META) {
+      if (!rt.meta.ptr)
+        aeisu::fail(AEISU_ERR_STATE, "the fused path keeps coefficients on chip; configure with "
+                                     "AEISU_FLAG_UNFUSED or AEISU_FLAG_KEEP_INTERMEDIATES to read them");
+      src = rt.meta.ptr;
+    } else {
       const int li = which - AEISU_BUF_LOW0;
       if (rt.nlow != 5 && li != 4) aeisu::fail(AEISU_ERR_STATE, "configure with AEISU_FLAG_KEEP_INTERMEDIATES to read this layer");
       src = rt.low[aeisu::low_slot(rt, li)].ptr;

@@ -49,7 +49,9 @@ def measured_traffic(config: int):
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes "):
                 _, name, value = line.split()
-                out["head" if name.startswith("head") else "refine_tail" if name.startswith("refine") else name] = int(value)
+                key = ("refine_tail_head" if name.startswith("fused") else "head" if name.startswith("head")
+                       else "refine_tail" if name.startswith("refine") else name)
+                out[key] = int(value)
     return out
 
 
@@ -94,6 +96,8 @@ def main():
     ap.add_argument("--pool", type=int, default=4, help="distinct resident frames cycled through")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replays")
+    ap.add_argument("--unfused", action="store_true",
+                    help="refine+tail and head as two kernels (coefficients through device memory)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (reference point for HBM counters)")
     args = ap.parse_args()
@@ -118,15 +122,17 @@ def main():
     model = R.load_model(ROOT / "weights" / wl["weights"], precision=wl["precision"])
     stream = torch.cuda.current_stream()
 
+    run_flags = L.FLAG_UNFUSED if args.unfused else 0
+
     def step(i, graph):
         j = i % len(pool)
-        model.run(pool[j], out=outs[j], graph=graph, check_finite=False)
+        model.run(pool[j], out=outs[j], graph=graph, check_finite=False, flags=run_flags)
 
     # --- 1. timed region: graph replays (or eager) --------------------------------------------------
     graph = not args.eager
     for i in range(args.warmup):
         step(i, graph)
-    model.run(pool[0], out=outs[0])                          # finite check once, outside timing
+    model.run(pool[0], out=outs[0], flags=run_flags)         # finite check once, outside timing
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -137,7 +143,7 @@ def main():
     log(f"bench: {ms_per_step:.4f} ms/step ({'graph' if graph else 'eager'})")
 
     # --- 2. per-kernel HIP events on the launch stream ---------------------------------------------
-    hd = model.handle(B, H, W, torch.float16, torch.float16, L.FLAG_STAGE_TIMING)
+    hd = model.handle(B, H, W, torch.float16, torch.float16, L.FLAG_STAGE_TIMING | run_flags)
     for i in range(min(args.warmup, 5)):
         L.check(L.lib().aeisu_upscale_async(hd.ptr, pool[i % len(pool)].data_ptr(), outs[i % len(pool)].data_ptr(),
                                             stream.cuda_stream))
@@ -159,25 +165,38 @@ def main():
     head_bytes = lr_px * (3 * s_io + 16 * 2 + 12 * s_io)      # RGB in + FP16 coefficients + 2x RGB out
     refine_bytes = packed_px * (32 * 2 + 64 * 2)              # FP16 refine input + FP16 coefficient output
     refine_flops = 2.0 * packed_px * (32 * 64 * 9 + 64 * 64)
+    synth_flops = 2.0 * lr_px * 16 * 100                      # head filter synthesis (MFMA)
     low_kind = {"fp16": "fp16", "mixed": "fp8", "int8": "int8"}[wl["precision"]]
     ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
     ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
     ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK["fp16"] + ctrl_flops_low / MFMA_PEAK[low_kind]
-    ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand", "refine_tail"))
-    head_s = stages["head"] / 1000
-    refine_s = stages["refine_tail"] / 1000
-    kernels = {
-        "head": {"bound": "hbm", "achieved": head_bytes / head_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                 "frac": head_bytes / head_s / HBM_PEAK, "ms": stages["head"],
-                 "algorithmic_bytes": head_bytes, "traffic": None},
-        "refine_tail": {"bound": "mfma", "achieved": refine_flops / refine_s / 1e12,
-                        "peak": MFMA_PEAK["fp16"] / 1e12, "unit": "TFLOP/s",
-                        "frac": refine_flops / refine_s / MFMA_PEAK["fp16"], "ms": stages["refine_tail"],
-                        "algorithmic_flops": refine_flops, "traffic": None},
-    }
+    fused = not args.unfused                                  # refine+tail+head in one kernel
     traffic = measured_traffic(args.config)
-    for k in kernels:
-        kernels[k]["traffic"] = traffic.get(k)
+    kernels = {}
+    if fused:
+        # work in + RGB in + 2x RGB out; coefficients never leave the chip
+        fused_bytes = packed_px * 32 * 2 + lr_px * (3 * s_io + 12 * s_io)
+        fs = stages["head"] / 1000
+        kernels["refine_tail_head"] = {
+            "bound": "hbm", "achieved": fused_bytes / fs / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": fused_bytes / fs / HBM_PEAK, "ms": stages["head"], "algorithmic_bytes": fused_bytes,
+            "traffic": traffic.get("refine_tail_head"),
+            "mfma_tflops": (refine_flops + synth_flops) / fs / 1e12,
+            "mfma_frac": (refine_flops + synth_flops) / fs / MFMA_PEAK["fp16"]}
+        ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand"))
+        stages.pop("refine_tail")                             # only the event-record gap; no kernel runs there
+        ctrl_ideal_s -= 2.0 * lr_px * (4608 + 1024) / MFMA_PEAK["fp16"]   # refine + tail run inside the fused kernel
+    else:
+        head_s = stages["head"] / 1000
+        refine_s = stages["refine_tail"] / 1000
+        kernels["head"] = {"bound": "hbm", "achieved": head_bytes / head_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                           "frac": head_bytes / head_s / HBM_PEAK, "ms": stages["head"],
+                           "algorithmic_bytes": head_bytes, "traffic": traffic.get("head")}
+        kernels["refine_tail"] = {"bound": "mfma", "achieved": refine_flops / refine_s / 1e12,
+                                  "peak": MFMA_PEAK["fp16"] / 1e12, "unit": "TFLOP/s",
+                                  "frac": refine_flops / refine_s / MFMA_PEAK["fp16"], "ms": stages["refine_tail"],
+                                  "algorithmic_flops": refine_flops, "traffic": traffic.get("refine_tail")}
+        ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand", "refine_tail"))
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     roof = {k: v for k, v in kernels[dominant].items() if k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
     roof["kernel"] = dominant
@@ -207,7 +226,8 @@ def main():
         "data": f"synthetic (aeisu_amd.frames config {args.config}, {args.pool} resident frames)",
         "config": {"workload": wl["name"], "config_id": args.config, "batch": B, "input": [3, H, W],
                    "output": [3, 2 * H, 2 * W], "precision": wl["precision"], "weights": wl["weights"],
-                   "timed": "graph replay" if graph else "eager"},
+                   "timed": "graph replay" if graph else "eager",
+                   "refine_tail_head": "two kernels" if args.unfused else "fused"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,

@@ -49,6 +49,10 @@ extern "C" {
 #define AEISU_FLAG_STAGE_TIMING 2u       /* record HIP events around each stage of every frame */
 #define AEISU_FLAG_NO_PAD 4u             /* input is already padded: FoldedAEISU.forward semantics
                                             (aeisu/model.py:546-551), full 2H x 2W output, H,W % 4 == 0 */
+#define AEISU_FLAG_UNFUSED 8u            /* run refine+tail and the head as two kernels with the
+                                            coefficient tensor in device memory (the reference
+                                            engine's structure); default: one fused kernel, the
+                                            coefficients stay on chip.  KEEP_INTERMEDIATES implies it */
 
 /* intermediates for aeisu_copy_intermediate */
 #define AEISU_BUF_SKIP 0   /* FP16 [B][Hp/2][Wp/2][32] project output */

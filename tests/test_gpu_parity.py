@@ -96,6 +96,27 @@ def test_head_phase_packing_exact(fp16_model, area_state):
 
 
 # ------------------------------------------------------------------------------------------------
+# fused refine + tail + head (coefficients on chip) vs the two-kernel path
+# ------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("h,w,b,fp32", [(72, 104, 1, False), (70, 102, 2, True), (37, 333, 1, False),
+                                         (540, 960, 1, False)])
+def test_fused_equals_unfused(mixed_model, fp16_model, h, w, b, fp32):
+    """Same arithmetic, same rounding points: the fused kernel must reproduce the two-kernel path bit for bit,
+    including odd padding offsets (70x102 -> py = px = 29) and frames narrower than one tile row."""
+    from aeisu_amd import _lib as L
+    say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
+    dt = torch.float32 if fp32 else torch.float16
+    frames = torch.stack([_frame(h, w, 40 + i) for i in range(b)]).to(dt).cuda().contiguous()
+    for model in (mixed_model, fp16_model):
+        fused = model.run(frames)
+        unfused = model.run(frames, flags=L.FLAG_UNFUSED)
+        torch.cuda.synchronize()
+        diff = (fused.float() - unfused.float()).abs().max().item()
+        say(f"  {model.precision}: max|fused - unfused| = {diff}")
+        assert torch.equal(fused, unfused)
+
+
+# ------------------------------------------------------------------------------------------------
 # controller and end-to-end, FP16 policy
 # ------------------------------------------------------------------------------------------------
 def test_controller_fp16_matches_emulation(fp16_model, area_state):
