@@ -49,8 +49,15 @@ def project_basis(raw: torch.Tensor, scale: float = 0.5) -> torch.Tensor:
     return (centred * (scale / norm)).permute(2, 0, 1).contiguous()
 
 
-def write(tensors: List[Tuple[str, int, int, np.ndarray]]) -> bytes:
-    """Serialise (name, dtype code, layout code, array) records into a SPYR8F8 blob."""
+def write(tensors: List[Tuple[str, int, int, np.ndarray]], edge_phase_max_shift: float = 0.0,
+          edge_gate_gain: float = 0.0) -> bytes:
+    """Serialise (name, dtype code, layout code, array) records into a SPYR8F8 blob.
+
+    Layout (SrcPyrModel.cpp:37-81): 512-byte header, one 80-byte descriptor per tensor,
+    payload from the first 64-byte boundary after the descriptors, every tensor at a
+    64-byte aligned offset in record order, file size padded to a multiple of 64 bytes;
+    SHA-256 of the file with its checksum field zeroed stored at byte 184.
+    """
     count = len(tensors)
     toc_bytes = count * DESC_SIZE
     payload = -(-(HEADER_SIZE + toc_bytes) // ALIGN) * ALIGN
@@ -58,11 +65,12 @@ def write(tensors: List[Tuple[str, int, int, np.ndarray]]) -> bytes:
     for _, _, _, arr in tensors:
         offsets.append(cursor)
         cursor = -(-(cursor + arr.nbytes) // ALIGN) * ALIGN
-    size = offsets[-1] + tensors[-1][3].nbytes if tensors else payload
+    size = cursor                                   # the file is padded to the alignment too
     blob = bytearray(size)
     dims = (8, 32, 32, 64, 4, 64, 2, 1, 1, 2, 1, count, ALIGN, DESC_SIZE)
     struct.pack_into("<8sIIII64s14I2f4Q", blob, 0, b"SPYR8F8\0", 1, HEADER_SIZE, 0x01020304, 0,
-                     ARCHITECTURE.encode(), *dims, 0.0, 0.0, size, HEADER_SIZE, toc_bytes, payload)
+                     ARCHITECTURE.encode(), *dims, edge_phase_max_shift, edge_gate_gain, size, HEADER_SIZE,
+                     toc_bytes, payload)
     for i, ((name, dtype, layout, arr), off) in enumerate(zip(tensors, offsets)):
         arr = np.ascontiguousarray(arr, dtype=_DTYPES[dtype])
         if len(name.encode()) >= 32 or arr.ndim == 0 or arr.ndim > 4:
@@ -166,6 +174,20 @@ def read_tensors(blob: bytes) -> Dict[str, np.ndarray]:
         arr = np.frombuffer(blob, dtype=_DTYPES[dtype], count=int(np.prod(shape)), offset=off)
         out[name.split(b"\0", 1)[0].decode()] = arr.reshape(shape)
     return out
+
+
+def read_records(blob: bytes) -> Tuple[List[Tuple[str, int, int, np.ndarray]], Dict[str, float]]:
+    """Ordered (name, dtype, layout, array) records and the edge-phase header fields of a
+    SPYR8F8 blob, such that ``write(records, **header) == blob`` for a well-formed file."""
+    count = struct.unpack_from("<I", blob, 132)[0]
+    shift, gain = struct.unpack_from("<2f", blob, 144)
+    records = []
+    for i in range(count):
+        name, dtype, layout, rank, *rest = struct.unpack_from("<32sIII4IQQ4s", blob, HEADER_SIZE + i * DESC_SIZE)
+        shape, off = tuple(rest[:4])[:rank], rest[4]
+        arr = np.frombuffer(blob, dtype=_DTYPES[dtype], count=int(np.prod(shape)), offset=off).reshape(shape)
+        records.append((name.split(b"\0", 1)[0].decode(), dtype, layout, arr.copy()))
+    return records, {"edge_phase_max_shift": shift, "edge_gate_gain": gain}
 
 
 def load_blob(path) -> Tuple[bytes, str]:

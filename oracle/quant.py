@@ -51,12 +51,13 @@ def e4m3_round(x) -> np.ndarray:
     v = np.asarray(x, dtype=np.float32).astype(np.float64)
     mag = np.abs(v)
     # exponent of the binade, floor(log2|v|), subnormal range pinned at -6
-    with np.errstate(divide="ignore"):
-        e = np.floor(np.log2(np.where(mag > 0, mag, 1.0)))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        e = np.floor(np.log2(np.where((mag > 0) & np.isfinite(mag), mag, 1.0)))
     e = np.maximum(e, -6.0)
     quantum = np.exp2(e - 3.0)
     q = np.round(mag / quantum) * quantum        # np.round is half-to-even; division exact
     q = np.minimum(q, E4M3_MAX)
+    q = np.where(np.isinf(mag), E4M3_MAX, q)      # SATFINITE: +-inf -> +-448
     out = np.copysign(q, v)
     out = np.where(np.isnan(v), np.nan, out)
     return out.astype(np.float32)
