@@ -1,0 +1,91 @@
+"""Evaluation-path pieces that need no GPU: encoded-Y PSNR/SSIM and image I/O.
+
+Definitions pinned against the reference (aeisu/metrics.py:11-39, aeisu/runtime.py:17-27,
+aeisu/data.py:14-29) by closed forms and a brute-force windowed SSIM written with loops.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from aeisu_amd import imageio as IO
+from aeisu_amd import metrics as MT
+
+
+def _ssim_bruteforce(a: np.ndarray, b: np.ndarray) -> float:
+    """Mean SSIM of two HW float64 arrays, valid 11x11 Gaussian (sigma 1.5) windows, explicit loops."""
+    g = np.exp(-((np.arange(11) - 5.0) ** 2) / (2 * 1.5 ** 2))
+    g /= g.sum()
+    w = np.outer(g, g)
+    vals = []
+    for y in range(a.shape[0] - 10):
+        for x in range(a.shape[1] - 10):
+            pa, pb = a[y:y + 11, x:x + 11], b[y:y + 11, x:x + 11]
+            ma, mb = (w * pa).sum(), (w * pb).sum()
+            va, vb = (w * pa * pa).sum() - ma * ma, (w * pb * pb).sum() - mb * mb
+            cv = (w * pa * pb).sum() - ma * mb
+            vals.append(((2 * ma * mb + 1e-4) * (2 * cv + 9e-4)) / ((ma * ma + mb * mb + 1e-4) * (va + vb + 9e-4)))
+    return float(np.mean(vals))
+
+
+def test_luma_closed_form():
+    white, black = torch.ones(3, 1, 1, dtype=torch.float64), torch.zeros(3, 1, 1, dtype=torch.float64)
+    assert MT.luma(white).item() == pytest.approx(235 / 255, abs=1e-12)
+    assert MT.luma(black).item() == pytest.approx(16 / 255, abs=1e-15)
+
+
+def test_distortion_against_bruteforce():
+    g = torch.Generator().manual_seed(2)
+    a = torch.rand(3, 21, 24, generator=g)
+    b = (a + 0.05 * torch.randn(3, 21, 24, generator=g)).clamp(0, 1)
+    got = MT.distortion(a, b, crop=2)
+    ya = MT.luma(a.double()[:, 2:-2, 2:-2])[0].numpy()
+    yb = MT.luma(b.double()[:, 2:-2, 2:-2])[0].numpy()
+    mse = float(((ya - yb) ** 2).mean())
+    assert got["y_mse"] == pytest.approx(mse, rel=1e-12)
+    assert got["y_psnr"] == pytest.approx(-10 * math.log10(mse), rel=1e-12)
+    assert got["y_ssim"] == pytest.approx(_ssim_bruteforce(ya, yb), abs=1e-12)
+    # the prediction is clamped, the target is not
+    assert MT.distortion(a * 3, b)["y_mse"] == pytest.approx(MT.distortion((a * 3).clamp(0, 1), b)["y_mse"])
+
+
+def test_distortion_identity_and_errors():
+    a = torch.rand(3, 16, 16)
+    same = MT.distortion(a, a, crop=2)
+    assert same["y_psnr"] == math.inf and same["y_ssim"] == pytest.approx(1.0, abs=1e-12)
+    with pytest.raises(ValueError):
+        MT.distortion(a, a[:, :15])
+    with pytest.raises(ValueError):
+        MT.distortion(a, torch.full_like(a, float("nan")))
+    with pytest.raises(ValueError):
+        MT.distortion(a[:, :14, :14], a[:, :14, :14], crop=2)          # 14 < 11 + 2 * 2
+    with pytest.raises(ValueError):
+        MT.distortion(a, a, crop=-1)
+
+
+def test_png_round_half_up_and_round_trip(tmp_path):
+    k = torch.arange(256, dtype=torch.float32)
+    img = (k / 255).view(1, 16, 16).expand(3, 16, 16).contiguous()
+    IO.save_rgb(tmp_path / "a.png", img)
+    back = IO.read_rgb(tmp_path / "a.png")
+    assert torch.equal(back, img)
+    half = torch.tensor([0.5 / 255, 0.4999 / 255, 254.5 / 255, 1.7, -0.2]).view(1, 1, 5).expand(3, 1, 5)
+    assert IO.quantize_u8(half)[0, :, 0].tolist() == [1, 0, 255, 255, 0]
+
+
+def test_paired_images(tmp_path):
+    for root in ("lr", "hr"):
+        (tmp_path / root / "sub").mkdir(parents=True)
+        IO.save_rgb(tmp_path / root / "sub" / "x.png", torch.zeros(3, 4, 4))
+    pairs = IO.paired_images(tmp_path / "lr", tmp_path / "hr")
+    assert [p[0].name for p in pairs] == ["x.png"]
+    IO.save_rgb(tmp_path / "lr" / "y.png", torch.zeros(3, 4, 4))
+    with pytest.raises(ValueError):
+        IO.paired_images(tmp_path / "lr", tmp_path / "hr")
+    IO.save_rgb(tmp_path / "hr" / "y.png", torch.zeros(3, 4, 4))
+    IO.save_rgb(tmp_path / "hr" / "y.jpg", torch.zeros(3, 4, 4))
+    with pytest.raises(ValueError):
+        IO.paired_images(tmp_path / "lr", tmp_path / "hr")
