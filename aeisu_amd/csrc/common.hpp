@@ -33,6 +33,9 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ f4 mfma_f16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f4 mfma_f16_k16(h4 a, h4 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ f4 mfma_fp8(long a, long b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(a, b, c, 0, 0, 0);
 }
@@ -45,14 +48,24 @@ __device__ __forceinline__ i4 mfma_i8(i4 a, i4 b, i4 c) {
 // Written as inline asm on purpose: with the ROCm 7.2 compiler the
 // __builtin_amdgcn_permlane{16,32}_swap builtin is treated as writing only its first result
 // (adding the two results is compiled into r[0] + r[0]).  Inline asm is opaque to the hazard
-// recognizer, so each swap carries the two wait states gfx950 needs between a VALU write of
-// either operand and the swap (without them the swap reads partially updated operands).
+// recognizer, so the asm carries the wait states itself: two before the swap (a VALU write of
+// either operand must settle; without them the swap reads partially updated operands) and,
+// in the *_mfma variants whose results feed an MFMA operand, five after it (the MFMA reads
+// its operands through a path that does not interlock with the swap's writes).
 #define AEISU_SWAP_ASM(op) asm volatile("s_nop 1\n\t" op " %0, %1" : "+v"(x), "+v"(y))
+#define AEISU_SWAP_ASM_MFMA(op) asm volatile("s_nop 1\n\t" op " %0, %1\n\ts_nop 4" : "+v"(x), "+v"(y))
 __device__ __forceinline__ void permlane32_swap(float& x, float& y) { AEISU_SWAP_ASM("v_permlane32_swap_b32"); }
 __device__ __forceinline__ void permlane16_swap(float& x, float& y) { AEISU_SWAP_ASM("v_permlane16_swap_b32"); }
 __device__ __forceinline__ void permlane32_swap_u(unsigned& x, unsigned& y) { AEISU_SWAP_ASM("v_permlane32_swap_b32"); }
 __device__ __forceinline__ void permlane16_swap_u(unsigned& x, unsigned& y) { AEISU_SWAP_ASM("v_permlane16_swap_b32"); }
+__device__ __forceinline__ void permlane32_swap_mfma(unsigned& x, unsigned& y) {
+  AEISU_SWAP_ASM_MFMA("v_permlane32_swap_b32");
+}
+__device__ __forceinline__ void permlane16_swap_mfma(unsigned& x, unsigned& y) {
+  AEISU_SWAP_ASM_MFMA("v_permlane16_swap_b32");
+}
 #undef AEISU_SWAP_ASM
+#undef AEISU_SWAP_ASM_MFMA
 
 // LeakyReLU as written by the reference epilogues: negative inputs scaled by the slope.
 __device__ __forceinline__ float leaky(float v, float slope) { return v < 0.0f ? v * slope : v; }

@@ -477,11 +477,13 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
     }
   }
 
-  // --- head bank: A1 = [K_hi | (0.05K)_hi] and A2 = [K_lo | (0.05K)_lo] fragments (against the
-  // kernel's B = [u ; w], clamp(a) = u + 0.05 w), followed by the learned base in accumulator
-  // layout.  Row m = 4g + i of tile t < 6 is (tap 4t + g, phase i); tile 6 row 4g is (tap 24,
-  // phase 2(g&1) + (g>>1)), the phase lane group g holds after the kernel's cross-lane
-  // reduction; the other rows of tile 6 are zero.
+  // --- head bank: two K=32 fragment sets of 7 row tiles each, FP32 accumulation in the kernel:
+  //   A1  = [K_hi | K_lo]                         against [u ; u]
+  //   A23 = slots 8g..8g+3: (0.05 K)_hi of coefficients 4g..4g+3, slots 4, 5: base_hi, base_lo
+  //                                               against the lane's own w and [1, 1] (group 0)
+  // (clamp(a) = u + 0.05 w in the kernel).  Row m = 4g + i of tile t < 6 is (tap 4t + g,
+  // phase i); tile 6 row 4g is (tap 24, phase 2(g&1) + (g>>1)), the phase lane group g holds
+  // after the kernel's cross-lane reduction; the other rows of tile 6 are zero.
   {
     const float* K = basis.f32();  // [25][16][4]
     const float* B = base.f32();   // [25][4]
@@ -494,27 +496,24 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
         ph = ((g & 1) << 1) | (g >> 1);
       }
     };
-    auto split = [](double v, bool want_lo) {
-      const uint16_t h = f32_to_f16_bits((float)v);
-      return want_lo ? f32_to_f16_bits((float)(v - (double)f16_bits_to_f32(h))) : h;
+    auto hi = [](double v) { return f32_to_f16_bits((float)v); };
+    auto lo = [](double v) {
+      return f32_to_f16_bits((float)(v - (double)f16_bits_to_f32(f32_to_f16_bits((float)v))));
     };
-    std::vector<uint16_t> frags = pack_frags<uint16_t>(14, 8, [&](int f, int m, int s) -> uint16_t {
+    rt.head.frag.upload(pack_frags<uint16_t>(14, 8, [&](int f, int m, int s) -> uint16_t {
       int tap, ph;
       row_of(f % 7, m, tap, ph);
       if (tap < 0) return 0;
-      const double k = K[(tap * 16 + (s & 15)) * 4 + ph];
-      return split(s < 16 ? k : 0.05 * k, f >= 7);
-    });
-    std::vector<uint8_t> img(frags.size() * 2 + 7 * 16 * sizeof(float));
-    std::memcpy(img.data(), frags.data(), frags.size() * 2);
-    float* bl = reinterpret_cast<float*>(img.data() + frags.size() * 2);
-    for (int t = 0; t < 7; ++t)
-      for (int m = 0; m < 16; ++m) {
-        int tap, ph;
-        row_of(t, m, tap, ph);
-        bl[t * 16 + m] = tap < 0 ? 0.f : B[tap * 4 + ph];
+      if (f < 7) {
+        const double k = K[(tap * 16 + (s & 15)) * 4 + ph];
+        return s < 16 ? hi(k) : lo(k);
       }
-    rt.head.frag.upload(img);
+      const int gs = s / 8, i = s % 8;
+      if (i < 4) return hi(0.05 * (double)K[(tap * 16 + 4 * gs + i) * 4 + ph]);
+      if (s == 4) return hi(B[tap * 4 + ph]);
+      if (s == 5) return lo(B[tap * 4 + ph]);
+      return 0;
+    }));
   }
 }
 
@@ -592,7 +591,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.refine = clamp_grid(refine_num_tiles(batch, rt.Hq, rt.Wq), refine_blocks_per_cu(), cus);
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
   rt.fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
-  rt.grid.fused = clamp_grid(fused_num_tiles(batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
+  rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
     rt.fused_ready = true;

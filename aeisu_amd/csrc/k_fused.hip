@@ -10,49 +10,71 @@
 //
 // Arithmetic is that of the unfused kernels (k_refine_tail.hip, k_head.hip): FP16 operands
 // with FP32 accumulation, FP32 refine bias, FP16-rounded tail bias, coefficients rounded to
-// FP16, then the head's exact clamp split and hi/lo bank synthesis.  The result is
-// bit-identical to refine_tail_kernel followed by head_kernel.
+// FP16, then the head's exact clamp split and MFMA synthesis.  The result is bit-identical
+// to refine_tail_kernel followed by head_kernel.
 //
-// gfx950 mapping: one persistent block of 12 waves per CU walks tiles of 32x4 packed pixels
-// (64x8 LR pixels) on the padded grid.
-//  * Waves 0-3 (producers) run refine + tail on the MFMA for tile i+1: the 44 weight
-//    fragments sit in LDS (45 KB, loaded once) and each fragment read feeds two 16-pixel
-//    groups; the refine accumulators become the tail's B operand in registers (the tail K
-//    order is permuted on the host); FP16 coefficients go to an LDS buffer.  They also
-//    load the zero-padded 34x6 work patch of tile i+2.
-//  * Waves 4-11 (consumers) run the head on tile i, one LR row each, reading coefficients
-//    and a clamped RGB tile from LDS, and load the RGB tile of tile i+1.
+// gfx950 mapping: one persistent block per CU walks tiles of 32 x QH packed pixels
+// (64 x 2QH LR pixels) on the padded grid.
+//  * 4 producer waves run refine + tail on the MFMA for tile i+1: the 44 weight fragments
+//    sit in LDS (45 KB, loaded once) and each fragment read feeds QH/2 16-pixel groups; the
+//    refine accumulators become the tail's B operand in registers (the tail K order is
+//    permuted on the host); FP16 coefficients go to an LDS buffer.  They also load the
+//    zero-padded work patch of tile i+2.
+//  * 2QH consumer waves run the head on tile i, one LR row each, reading coefficients and a
+//    clamped RGB tile from LDS, and load the RGB tile of tile i+1.
 //  * Work patch, coefficients and RGB tile are double-buffered; one barrier per tile.
 //    MFMA-bound producers and VALU-bound consumers share each SIMD.
+//  * FP16 frames: QH = 6 (16 waves, 4 per SIMD, <= 128 VGPRs), the RGB tile stays FP16 in
+//    LDS and the head's FMAs take it as a mixed-precision operand (v_fma_mix, exact);
+//    FP32 frames: QH = 4 (12 waves) with an FP32 RGB tile.
 #include "common.hpp"
 
 namespace aeisu {
 
-constexpr int kFQW = 32, kFQH = 4;                   // packed tile
-constexpr int kFPW = kFQW + 2, kFPH = kFQH + 2;      // work patch (1-pixel zero halo)
+template <typename Tin>
+struct FusedCfg;
+template <>
+struct FusedCfg<_Float16> {
+  static constexpr int QH = 6;
+  typedef h4 Rgb;
+};
+template <>
+struct FusedCfg<float> {
+  static constexpr int QH = 4;
+  typedef float4 Rgb;
+};
+
+constexpr int kFQW = 32;                             // packed tile width
 constexpr int kFPix = 40;                            // halves per patch pixel (32 + 8 pad)
 constexpr int kFMPix = 72;                           // halves per coefficient pixel (64 + 8 pad)
-constexpr int kFLW = 2 * kFQW, kFLH = 2 * kFQH;      // LR tile
-constexpr int kFRW = kFLW + 4, kFRH = kFLH + 4;      // RGB tile (2-pixel clamped halo)
-constexpr int kFRPos = kFRW * kFRH;
-constexpr int kFThreads = 768, kFProducers = 4;
-constexpr int kFConsumerThreads = kFThreads - 64 * kFProducers;
-constexpr int kFRgbPer = (kFRPos + kFConsumerThreads - 1) / kFConsumerThreads;
-constexpr int kFPatchChunks = kFPH * kFPW * 4;       // 16-byte chunks of one work patch
-constexpr int kFPatchPer = (kFPatchChunks + 64 * kFProducers - 1) / (64 * kFProducers);
+constexpr int kFLW = 2 * kFQW, kFRW = kFLW + 4;      // LR tile width, RGB tile width (2-pixel halo)
+constexpr int kFProducers = 4;
 constexpr int kFRefineFrags = 36, kFTailFrags = 8;
-
-// LDS layout (bytes)
-constexpr int kFOffW = 0;
 constexpr int kFSizeW = (kFRefineFrags + kFTailFrags) * 64 * 16;
-constexpr int kFOffPatch = kFOffW + kFSizeW;
-constexpr int kFSizePatch = kFPH * kFPW * kFPix * 2;
-constexpr int kFOffMeta = kFOffPatch + 2 * kFSizePatch;
-constexpr int kFSizeMeta = kFQH * kFQW * kFMPix * 2;
-constexpr int kFOffRgb = kFOffMeta + 2 * kFSizeMeta;
-constexpr int kFSizeRgb = kFRPos * 16;
-constexpr int kFLds = kFOffRgb + 2 * kFSizeRgb;
-static_assert(kFLds <= 160 * 1024, "fused kernel LDS exceeds the CU's 160 KB");
+
+template <typename Tin>
+struct FusedLayout {
+  static constexpr int QH = FusedCfg<Tin>::QH;
+  static constexpr int LH = 2 * QH, RH = LH + 4, RPos = kFRW * RH;
+  static constexpr int PH = QH + 2, PW = kFQW + 2;
+  static constexpr int Consumers = LH, Threads = 64 * (kFProducers + Consumers);
+  static constexpr int ConsumerThreads = 64 * Consumers;
+  static constexpr int J = QH / 2;                   // 16-pixel groups per producer (2 per packed row)
+  static constexpr int RgbPer = (RPos + ConsumerThreads - 1) / ConsumerThreads;
+  static constexpr int PatchChunks = PH * PW * 4;    // 16-byte chunks of one work patch
+  static constexpr int PatchPer = (PatchChunks + 64 * kFProducers - 1) / (64 * kFProducers);
+  static constexpr int OffW = 0;
+  static constexpr int OffBias = OffW + kFSizeW;     // refine bias [64], tail bias [64] (FP32)
+  static constexpr int OffPatch = OffBias + 512;
+  static constexpr int SizePatch = PH * PW * kFPix * 2;
+  static constexpr int OffMeta = OffPatch + 2 * SizePatch;
+  static constexpr int SizeMeta = QH * kFQW * kFMPix * 2;
+  static constexpr int OffRgb = OffMeta + 2 * SizeMeta;
+  static constexpr int SizeRgb = RPos * (int)sizeof(typename FusedCfg<Tin>::Rgb);
+  static constexpr int Lds = OffRgb + 2 * SizeRgb;
+  static_assert(Lds <= 160 * 1024, "fused kernel LDS exceeds the CU's 160 KB");
+  static_assert(J * kFProducers == 2 * QH, "producers must split the tile's 16-pixel groups evenly");
+};
 
 struct FusedGeom {
   int H, W, Hq, Wq, py, px, batch;
@@ -62,32 +84,32 @@ struct FusedGeom {
 struct FusedTile {
   int b, qy0, qx0;
 };
+template <int QH>
 __device__ __forceinline__ FusedTile fused_tile(int tidx, const FusedGeom& G) {
   FusedTile t;
   t.b = tidx / (G.tiles_y * G.tiles_x);
   const int rem = tidx - t.b * G.tiles_y * G.tiles_x;
-  t.qy0 = G.qy_lo + (rem / G.tiles_x) * kFQH;
+  t.qy0 = G.qy_lo + (rem / G.tiles_x) * QH;
   t.qx0 = G.qx_lo + (rem % G.tiles_x) * kFQW;
   return t;
 }
 
-template <typename Tin>
-__device__ __forceinline__ float fload(const Tin* p) { return (float)*p; }
-
 // ---- producer side ----------------------------------------------------------------------------
+template <typename LY>
 struct PatchRegs {
-  u4 v[kFPatchPer];
+  u4 v[LY::PatchPer];
 };
-__device__ __forceinline__ void patch_fetch(PatchRegs& r, const _Float16* __restrict__ work, FusedTile t,
+template <typename LY>
+__device__ __forceinline__ void patch_fetch(PatchRegs<LY>& r, const _Float16* __restrict__ work, FusedTile t,
                                             const FusedGeom& G, int ptid) {
   const _Float16* in = work + (size_t)t.b * G.Hq * G.Wq * 32;
 #pragma unroll
-  for (int k = 0; k < kFPatchPer; ++k) {
+  for (int k = 0; k < LY::PatchPer; ++k) {
     const int q = ptid + 64 * kFProducers * k;
     u4 v = {0u, 0u, 0u, 0u};
-    if (q < kFPatchChunks) {
+    if (q < LY::PatchChunks) {
       const int pix = q >> 2, ch = (q & 3) * 8;
-      const int ly = pix / kFPW, lx = pix - ly * kFPW;
+      const int ly = pix / LY::PW, lx = pix - ly * LY::PW;
       const int gy = t.qy0 + ly - 1, gx = t.qx0 + lx - 1;
       if (gy >= 0 && gy < G.Hq && gx >= 0 && gx < G.Wq)
         v = *reinterpret_cast<const u4*>(in + ((size_t)gy * G.Wq + gx) * 32 + ch);
@@ -95,86 +117,109 @@ __device__ __forceinline__ void patch_fetch(PatchRegs& r, const _Float16* __rest
     r.v[k] = v;
   }
 }
-__device__ __forceinline__ void patch_store(const PatchRegs& r, unsigned char* lds_patch, int ptid) {
+template <typename LY>
+__device__ __forceinline__ void patch_store(const PatchRegs<LY>& r, unsigned char* lds_patch, int ptid) {
 #pragma unroll
-  for (int k = 0; k < kFPatchPer; ++k) {
+  for (int k = 0; k < LY::PatchPer; ++k) {
     const int q = ptid + 64 * kFProducers * k;
-    if (q < kFPatchChunks) {
+    if (q < LY::PatchChunks) {
       const int pix = q >> 2, ch = (q & 3) * 8;
       *reinterpret_cast<u4*>(lds_patch + (pix * kFPix + ch) * 2) = r.v[k];
     }
   }
 }
 
-// refine + tail for packed row `prow` of the tile (two 16-pixel groups) -> FP16 coefficients.
-__device__ __forceinline__ void produce_row(const unsigned char* lds_w, const unsigned char* lds_patch,
-                                            unsigned char* lds_meta, int prow, int lane,
-                                            const float (&rb)[4][4], const float (&tb)[4][4]) {
+// refine + tail for 16-pixel groups p*J .. p*J+J-1 of the tile (group q: packed row q/2, half q%2)
+template <typename LY>
+__device__ __forceinline__ void produce(const unsigned char* smem, const unsigned char* lds_patch,
+                                        unsigned char* lds_meta, int p, int lane) {
+  constexpr int J = LY::J;
   const int n = lane & 15, g = lane >> 4;
-  const h8* wf = reinterpret_cast<const h8*>(lds_w);
-  const _Float16(*patch)[kFPW][kFPix] = reinterpret_cast<const _Float16(*)[kFPW][kFPix]>(lds_patch);
-  f4 acc[4][2];
+  const h8* wf = reinterpret_cast<const h8*>(smem + LY::OffW);
+  const f4* bias = reinterpret_cast<const f4*>(smem + LY::OffBias);
+  const _Float16(*patch)[LY::PW][kFPix] = reinterpret_cast<const _Float16(*)[LY::PW][kFPix]>(lds_patch);
+  int prow[J], pcol[J];
 #pragma unroll
-  for (int T = 0; T < 4; ++T) acc[T][0] = acc[T][1] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int jj = 0; jj < J; ++jj) {
+    const int q = p * J + jj;
+    prow[jj] = q >> 1;
+    pcol[jj] = 16 * (q & 1);
+  }
+  f4 acc[4][J];
+#pragma unroll
+  for (int T = 0; T < 4; ++T)
+#pragma unroll
+    for (int jj = 0; jj < J; ++jj) acc[T][jj] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int k = 0; k < 9; ++k) {
-    const h8 b0 = *reinterpret_cast<const h8*>(&patch[prow + k / 3][n + k % 3][8 * g]);
-    const h8 b1 = *reinterpret_cast<const h8*>(&patch[prow + k / 3][16 + n + k % 3][8 * g]);
+    h8 b[J];
+#pragma unroll
+    for (int jj = 0; jj < J; ++jj)
+      b[jj] = *reinterpret_cast<const h8*>(&patch[prow[jj] + k / 3][pcol[jj] + n + k % 3][8 * g]);
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
       const h8 a = wf[(T * 9 + k) * 64 + lane];
-      acc[T][0] = mfma_f16(a, b0, acc[T][0]);
-      acc[T][1] = mfma_f16(a, b1, acc[T][1]);
+#pragma unroll
+      for (int jj = 0; jj < J; ++jj) acc[T][jj] = mfma_f16(a, b[jj], acc[T][jj]);
     }
   }
 #pragma unroll
-  for (int J = 0; J < 2; ++J) {
+  for (int jj = 0; jj < J; ++jj) {
     h8 bt[2];
 #pragma unroll
-    for (int T = 0; T < 4; ++T)
+    for (int T = 0; T < 4; ++T) {
+      const f4 rb = bias[4 * T + g];                 // refine bias of channels 16T + 4g + r
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bt[T >> 1][(T & 1) * 4 + r] = (_Float16)leaky(acc[T][J][r] + rb[T][r], 0.1f);
-    _Float16* dst = reinterpret_cast<_Float16*>(lds_meta) + ((prow * kFQW) + 16 * J + n) * kFMPix + 4 * g;
+      for (int r = 0; r < 4; ++r) bt[T >> 1][(T & 1) * 4 + r] = (_Float16)leaky(acc[T][jj][r] + rb[r], 0.1f);
+    }
+    _Float16* dst = reinterpret_cast<_Float16*>(lds_meta) + (prow[jj] * kFQW + pcol[jj] + n) * kFMPix + 4 * g;
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
       f4 o = mfma_f16(wf[(kFRefineFrags + T * 2) * 64 + lane], bt[0], f4{0.f, 0.f, 0.f, 0.f});
       o = mfma_f16(wf[(kFRefineFrags + T * 2 + 1) * 64 + lane], bt[1], o);
+      const f4 tb = bias[16 + 4 * T + g];            // FP16-rounded tail bias
       u2 w;
-      w[0] = pack_h2(o[0] + tb[T][0], o[1] + tb[T][1]);
-      w[1] = pack_h2(o[2] + tb[T][2], o[3] + tb[T][3]);
+      w[0] = pack_h2(o[0] + tb[0], o[1] + tb[1]);
+      w[1] = pack_h2(o[2] + tb[2], o[3] + tb[3]);
       *reinterpret_cast<u2*>(dst + 16 * T) = w;
     }
   }
 }
 
 // ---- consumer side ----------------------------------------------------------------------------
+template <typename LY>
 struct RgbRegs {
-  float v[kFRgbPer][3];
+  float v[LY::RgbPer][3];
 };
-template <typename Tin>
-__device__ __forceinline__ void rgb_fetch(RgbRegs& r, const Tin* __restrict__ src, FusedTile t, const FusedGeom& G,
-                                          int ctid) {
+template <typename Tin, typename LY>
+__device__ __forceinline__ void rgb_fetch(RgbRegs<LY>& r, const Tin* __restrict__ src, FusedTile t,
+                                          const FusedGeom& G, int ctid) {
   const size_t plane = (size_t)G.H * G.W;
   const Tin* s = src + (size_t)t.b * 3 * plane;
   const int y0 = 2 * t.qy0 - G.py - 2, x0 = 2 * t.qx0 - G.px - 2;
 #pragma unroll
-  for (int k = 0; k < kFRgbPer; ++k) {
-    const int q = ctid + kFConsumerThreads * k;
-    if (q < kFRPos) {
+  for (int k = 0; k < LY::RgbPer; ++k) {
+    const int q = ctid + LY::ConsumerThreads * k;
+    if (q < LY::RPos) {
       const int ly = q / kFRW, lx = q - ly * kFRW;
       const int sy = min(max(y0 + ly, 0), G.H - 1), sx = min(max(x0 + lx, 0), G.W - 1);
       const size_t o = (size_t)sy * G.W + sx;
-      r.v[k][0] = fload(s + o);
-      r.v[k][1] = fload(s + plane + o);
-      r.v[k][2] = fload(s + 2 * plane + o);
+      r.v[k][0] = (float)s[o];
+      r.v[k][1] = (float)s[plane + o];
+      r.v[k][2] = (float)s[2 * plane + o];
     }
   }
 }
-__device__ __forceinline__ void rgb_store(const RgbRegs& r, float4* lds_rgb, int ctid) {
+__device__ __forceinline__ void rgb_put(h4* d, float a, float b, float c) {
+  *d = h4{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)0.0f};   // exact: the values came from FP16
+}
+__device__ __forceinline__ void rgb_put(float4* d, float a, float b, float c) { *d = make_float4(a, b, c, 0.f); }
+template <typename Rgb, typename LY>
+__device__ __forceinline__ void rgb_store(const RgbRegs<LY>& r, Rgb* lds_rgb, int ctid) {
 #pragma unroll
-  for (int k = 0; k < kFRgbPer; ++k) {
-    const int q = ctid + kFConsumerThreads * k;
-    if (q < kFRPos) lds_rgb[q] = make_float4(r.v[k][0], r.v[k][1], r.v[k][2], 0.f);
+  for (int k = 0; k < LY::RgbPer; ++k) {
+    const int q = ctid + LY::ConsumerThreads * k;
+    if (q < LY::RPos) rgb_put(lds_rgb + q, r.v[k][0], r.v[k][1], r.v[k][2]);
   }
 }
 
@@ -208,10 +253,10 @@ __device__ __forceinline__ void fstore_pair<float>(float* p, float left, float r
 }
 
 // Head on LR row `r` of the tile.
-template <typename Tout>
-__device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const float4* lds_rgb, Tout* __restrict__ out,
+template <typename Tout, typename Rgb>
+__device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const Rgb* lds_rgb, Tout* __restrict__ out,
                                             FusedTile t, const FusedGeom& G, int r, int lane, const h8 (&A1)[7],
-                                            const h8 (&A2)[7], const f4 (&base)[7], const int (&toff)[6],
+                                            const h8 (&A23)[7], const unsigned ones, const int (&toff)[6],
                                             float& chk) {
   const int n = lane & 15, g = lane >> 4;
   const int y = 2 * t.qy0 + r - G.py;
@@ -229,30 +274,33 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     unsigned U[2], Wd[2];
     fused_clamp_split(coef[0], U[0], Wd[0]);
     fused_clamp_split(coef[1], U[1], Wd[1]);
+    unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
 #pragma unroll
-    for (int w = 0; w < 2; ++w) permlane32_swap_u(U[w], Wd[w]);
+    for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
 #pragma unroll
-    for (int w = 0; w < 2; ++w) permlane16_swap_u(U[w], Wd[w]);
-    const u4 bw = {U[0], U[1], Wd[0], Wd[1]};
-    const h8 bop = __builtin_bit_cast(h8, bw);
+    for (int w = 0; w < 2; ++w) permlane16_swap_mfma(Ux[w], Uy[w]);
+    const u4 bu = {Ux[0], Ux[1], Uy[0], Uy[1]};
+    const u4 bw = {Wd[0], Wd[1], ones, 0u};
+    const h8 bop_u = __builtin_bit_cast(h8, bu);
+    const h8 bop_w = __builtin_bit_cast(h8, bw);
     f4 acc[7];
 #pragma unroll
     for (int q = 0; q < 7; ++q) {
-      acc[q] = mfma_f16(A1[q], bop, base[q]);
-      acc[q] = mfma_f16(A2[q], bop, acc[q]);
+      acc[q] = mfma_f16(A1[q], bop_u, f4{0.f, 0.f, 0.f, 0.f});
+      acc[q] = mfma_f16(A23[q], bop_w, acc[q]);
     }
-    const float4* L0 = lds_rgb + r * kFRW + 16 * j + n;
+    const Rgb* L0 = lds_rgb + r * kFRW + 16 * j + n;
     float o[12];
 #pragma unroll
     for (int i = 0; i < 12; ++i) o[i] = 0.f;
 #pragma unroll
     for (int q = 0; q < 6; ++q) {
-      const float4 L = L0[toff[q]];
+      const Rgb L = L0[toff[q]];
 #pragma unroll
       for (int ph = 0; ph < 4; ++ph) {
-        o[0 * 4 + ph] = fmaf(acc[q][ph], L.x, o[0 * 4 + ph]);
-        o[1 * 4 + ph] = fmaf(acc[q][ph], L.y, o[1 * 4 + ph]);
-        o[2 * 4 + ph] = fmaf(acc[q][ph], L.z, o[2 * 4 + ph]);
+        o[0 * 4 + ph] = fmaf(acc[q][ph], (float)L.x, o[0 * 4 + ph]);
+        o[1 * 4 + ph] = fmaf(acc[q][ph], (float)L.y, o[1 * 4 + ph]);
+        o[2 * 4 + ph] = fmaf(acc[q][ph], (float)L.z, o[2 * 4 + ph]);
       }
     }
     float s[6];
@@ -269,10 +317,10 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       permlane16_swap(a, z);
       u[c] = a + z;
     }
-    const float4 L24 = L0[4 * kFRW + 4];
-    u[0] = fmaf(acc[6][0], L24.x, u[0]);
-    u[1] = fmaf(acc[6][0], L24.y, u[1]);
-    u[2] = fmaf(acc[6][0], L24.z, u[2]);
+    const Rgb L24 = L0[4 * kFRW + 4];
+    u[0] = fmaf(acc[6][0], (float)L24.x, u[0]);
+    u[1] = fmaf(acc[6][0], (float)L24.y, u[1]);
+    u[2] = fmaf(acc[6][0], (float)L24.z, u[2]);
     const bool inside = x >= 0 && x < G.W;
     chk = fmaf(inside ? u[0] + u[1] + u[2] : 0.f, 0.0f, chk);
     float left[3], right[3];
@@ -291,44 +339,35 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
 }
 
 // Producer waves: coefficients of tile i+1, work patch of tile i+2.
+template <typename Tin>
 __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float16* __restrict__ work,
-                                              const float* __restrict__ rbias, const float* __restrict__ tbias,
                                               const FusedGeom& G, int wave, int lane, int ptid) {
-  const int g = lane >> 4;
-  float rb[4][4], tb[4][4];
-#pragma unroll
-  for (int T = 0; T < 4; ++T)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      rb[T][r] = rbias[16 * T + 4 * g + r];
-      tb[T][r] = tbias[16 * T + 4 * g + r];
-    }
-  unsigned char* const lds_w = smem + kFOffW;
+  typedef FusedLayout<Tin> LY;
   const int t0 = tile_of(0, G.num_tiles), t1 = tile_of(1, G.num_tiles);
   {
-    PatchRegs pr;
+    PatchRegs<LY> pr;
     if (t0 < G.num_tiles) {
-      patch_fetch(pr, work, fused_tile(t0, G), G, ptid);
-      patch_store(pr, smem + kFOffPatch, ptid);
+      patch_fetch<LY>(pr, work, fused_tile<LY::QH>(t0, G), G, ptid);
+      patch_store<LY>(pr, smem + LY::OffPatch, ptid);
     }
     if (t1 < G.num_tiles) {
-      patch_fetch(pr, work, fused_tile(t1, G), G, ptid);
-      patch_store(pr, smem + kFOffPatch + kFSizePatch, ptid);
+      patch_fetch<LY>(pr, work, fused_tile<LY::QH>(t1, G), G, ptid);
+      patch_store<LY>(pr, smem + LY::OffPatch + LY::SizePatch, ptid);
     }
   }
-  __syncthreads();                                   // prologue loads visible
-  if (t0 < G.num_tiles) produce_row(lds_w, smem + kFOffPatch, smem + kFOffMeta, wave, lane, rb, tb);
+  __syncthreads();                                   // weights, biases and prologue loads visible
+  if (t0 < G.num_tiles) produce<LY>(smem, smem + LY::OffPatch, smem + LY::OffMeta, wave, lane);
   __syncthreads();                                   // coefficients of tile 0 visible
   const int iters = tile_iters(G.num_tiles);
   for (int it = 0; it < iters; ++it) {
     if (tile_of(it, G.num_tiles) >= G.num_tiles) break;   // block-uniform, as in consumer_main
     const int tn = tile_of(it + 1, G.num_tiles), tnn = tile_of(it + 2, G.num_tiles);
     const int cur = it & 1, nxt = cur ^ 1;
-    PatchRegs pr;
-    if (tnn < G.num_tiles) patch_fetch(pr, work, fused_tile(tnn, G), G, ptid);
+    PatchRegs<LY> pr;
+    if (tnn < G.num_tiles) patch_fetch<LY>(pr, work, fused_tile<LY::QH>(tnn, G), G, ptid);
     if (tn < G.num_tiles)
-      produce_row(lds_w, smem + kFOffPatch + nxt * kFSizePatch, smem + kFOffMeta + nxt * kFSizeMeta, wave, lane, rb, tb);
-    if (tnn < G.num_tiles) patch_store(pr, smem + kFOffPatch + cur * kFSizePatch, ptid);
+      produce<LY>(smem, smem + LY::OffPatch + nxt * LY::SizePatch, smem + LY::OffMeta + nxt * LY::SizeMeta, wave, lane);
+    if (tnn < G.num_tiles) patch_store<LY>(pr, smem + LY::OffPatch + cur * LY::SizePatch, ptid);
     __syncthreads();
   }
 }
@@ -339,17 +378,17 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
                                               const h8* __restrict__ bankA, Tout* __restrict__ out,
                                               const FusedGeom& G, int row, int lane, int ctid,
                                               unsigned* __restrict__ nonfinite) {
+  typedef FusedLayout<Tin> LY;
+  typedef typename FusedCfg<Tin>::Rgb Rgb;
   const int g = lane >> 4;
-  h8 A1[7], A2[7];
-  f4 base[7];
+  h8 A1[7], A23[7];
   int toff[6];
-  const f4* base_src = reinterpret_cast<const f4*>(bankA + 14 * 64);
 #pragma unroll
   for (int q = 0; q < 7; ++q) {
     A1[q] = bankA[q * 64 + lane];
-    A2[q] = bankA[(7 + q) * 64 + lane];
-    base[q] = base_src[q * 4 + g];
+    A23[q] = bankA[(7 + q) * 64 + lane];
   }
+  const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
 #pragma unroll
   for (int q = 0; q < 6; ++q) {
     const int tap = 4 * q + g;
@@ -358,9 +397,9 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
   float chk = 0.f;
   const int t0 = tile_of(0, G.num_tiles);
   if (t0 < G.num_tiles) {
-    RgbRegs rr;
-    rgb_fetch(rr, src, fused_tile(t0, G), G, ctid);
-    rgb_store(rr, reinterpret_cast<float4*>(smem + kFOffRgb), ctid);
+    RgbRegs<LY> rr;
+    rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(t0, G), G, ctid);
+    rgb_store<Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb), ctid);
   }
   __syncthreads();                                   // prologue loads visible
   __syncthreads();                                   // coefficients of tile 0 visible
@@ -370,11 +409,12 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
     if (tc >= G.num_tiles) break;                    // block-uniform, as in producer_main
     const int tn = tile_of(it + 1, G.num_tiles);
     const int cur = it & 1, nxt = cur ^ 1;
-    RgbRegs rr;
-    if (tn < G.num_tiles) rgb_fetch(rr, src, fused_tile(tn, G), G, ctid);
-    consume_row<Tout>(smem + kFOffMeta + cur * kFSizeMeta, reinterpret_cast<const float4*>(smem + kFOffRgb + cur * kFSizeRgb),
-                      out, fused_tile(tc, G), G, row, lane, A1, A2, base, toff, chk);
-    if (tn < G.num_tiles) rgb_store(rr, reinterpret_cast<float4*>(smem + kFOffRgb + nxt * kFSizeRgb), ctid);
+    RgbRegs<LY> rr;
+    if (tn < G.num_tiles) rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(tn, G), G, ctid);
+    consume_row<Tout, Rgb>(smem + LY::OffMeta + cur * LY::SizeMeta,
+                           reinterpret_cast<const Rgb*>(smem + LY::OffRgb + cur * LY::SizeRgb), out,
+                           fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, ones, toff, chk);
+    if (tn < G.num_tiles) rgb_store<Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
     __syncthreads();
   }
   if (nonfinite && __ballot(chk != chk) != 0ull && lane == 0) atomicOr(nonfinite, 1u);
@@ -382,44 +422,51 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
 
 // Every wave executes the same number of barriers: two in the prologue, one per tile.
 template <typename Tin, typename Tout>
-__global__ __launch_bounds__(kFThreads) void fused_tail_head_kernel(
+__global__ __launch_bounds__(FusedLayout<Tin>::Threads) void fused_tail_head_kernel(
     const _Float16* __restrict__ work, const Tin* __restrict__ src, const h8* __restrict__ rt_frag,
     const float* __restrict__ rbias, const float* __restrict__ tbias, const h8* __restrict__ bankA,
     Tout* __restrict__ out, FusedGeom G, unsigned* __restrict__ nonfinite) {
+  typedef FusedLayout<Tin> LY;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   {
     const u4* s = reinterpret_cast<const u4*>(rt_frag);
-    u4* d = reinterpret_cast<u4*>(smem + kFOffW);
-    for (int i = tid; i < kFSizeW / 16; i += kFThreads) d[i] = s[i];
+    u4* d = reinterpret_cast<u4*>(smem + LY::OffW);
+    for (int i = tid; i < kFSizeW / 16; i += LY::Threads) d[i] = s[i];
+    float* b = reinterpret_cast<float*>(smem + LY::OffBias);
+    if (tid < 64) b[tid] = rbias[tid];
+    else if (tid < 128) b[tid] = tbias[tid - 64];
   }
   if (wave < kFProducers)                            // wave-uniform role
-    producer_main(smem, work, rbias, tbias, G, wave, lane, tid);
+    producer_main<Tin>(smem, work, G, wave, lane, tid);
   else
     consumer_main<Tin, Tout>(smem, src, bankA, out, G, wave - kFProducers, lane, tid - 64 * kFProducers, nonfinite);
 }
 
-FusedGeom fused_geometry(int H, int W, int Hq, int Wq, int py, int px, int batch) {
+static FusedGeom fused_geometry(int qh, int H, int W, int Hq, int Wq, int py, int px, int batch) {
   FusedGeom G;
   G.H = H; G.W = W; G.Hq = Hq; G.Wq = Wq; G.py = py; G.px = px; G.batch = batch;
   G.qy_lo = py >> 1;
   G.qx_lo = px >> 1;
   const int qy_hi = (py + H - 1) >> 1, qx_hi = (px + W - 1) >> 1;
-  G.tiles_y = (qy_hi - G.qy_lo + kFQH) / kFQH;
+  G.tiles_y = (qy_hi - G.qy_lo + qh) / qh;
   G.tiles_x = (qx_hi - G.qx_lo + kFQW) / kFQW;
   G.num_tiles = batch * G.tiles_y * G.tiles_x;
   return G;
 }
 
-int fused_num_tiles(int batch, int H, int W, int Hq, int Wq, int py, int px) {
-  return fused_geometry(H, W, Hq, Wq, py, px, batch).num_tiles;
+int fused_num_tiles(int in_fp32, int batch, int H, int W, int Hq, int Wq, int py, int px) {
+  const int qh = in_fp32 ? FusedCfg<float>::QH : FusedCfg<_Float16>::QH;
+  return fused_geometry(qh, H, W, Hq, Wq, py, px, batch).num_tiles;
 }
 
 template <typename Tin, typename Tout>
 static hipError_t launch_fused_t(const void* work, const void* src, const void* rt_frag, const float* rbias,
-                                 const float* tbias, const void* bankA, void* out, const FusedGeom& G,
-                                 unsigned* nonfinite, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((fused_tail_head_kernel<Tin, Tout>), dim3(grid), dim3(kFThreads), kFLds, stream,
+                                 const float* tbias, const void* bankA, void* out, int H, int W, int Hq, int Wq,
+                                 int py, int px, int batch, unsigned* nonfinite, int grid, hipStream_t stream) {
+  typedef FusedLayout<Tin> LY;
+  const FusedGeom G = fused_geometry(LY::QH, H, W, Hq, Wq, py, px, batch);
+  hipLaunchKernelGGL((fused_tail_head_kernel<Tin, Tout>), dim3(grid), dim3(LY::Threads), LY::Lds, stream,
                      (const _Float16*)work, (const Tin*)src, (const h8*)rt_frag, rbias, tbias, (const h8*)bankA,
                      (Tout*)out, G, nonfinite);
   return hipGetLastError();
@@ -431,8 +478,10 @@ hipError_t fused_prepare() {
                       reinterpret_cast<const void*>(&fused_tail_head_kernel<float, _Float16>),
                       reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, float>),
                       reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, _Float16>)};
-  for (const void* f : k) {
-    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFLds);
+  const int lds[4] = {FusedLayout<float>::Lds, FusedLayout<float>::Lds, FusedLayout<_Float16>::Lds,
+                      FusedLayout<_Float16>::Lds};
+  for (int i = 0; i < 4; ++i) {
+    const hipError_t e = hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize, lds[i]);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -442,14 +491,13 @@ hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, const void* work, c
                                   const float* rbias, const float* tbias, const void* bankA, void* out, int H, int W,
                                   int Hq, int Wq, int py, int px, int batch, unsigned* nonfinite, int grid,
                                   hipStream_t stream) {
-  const FusedGeom G = fused_geometry(H, W, Hq, Wq, py, px, batch);
-  if (in_fp32 && out_fp32)
-    return launch_fused_t<float, float>(work, src, rt_frag, rbias, tbias, bankA, out, G, nonfinite, grid, stream);
-  if (in_fp32)
-    return launch_fused_t<float, _Float16>(work, src, rt_frag, rbias, tbias, bankA, out, G, nonfinite, grid, stream);
-  if (out_fp32)
-    return launch_fused_t<_Float16, float>(work, src, rt_frag, rbias, tbias, bankA, out, G, nonfinite, grid, stream);
-  return launch_fused_t<_Float16, _Float16>(work, src, rt_frag, rbias, tbias, bankA, out, G, nonfinite, grid, stream);
+#define AEISU_FUSED(TI, TO) \
+  launch_fused_t<TI, TO>(work, src, rt_frag, rbias, tbias, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream)
+  if (in_fp32 && out_fp32) return AEISU_FUSED(float, float);
+  if (in_fp32) return AEISU_FUSED(float, _Float16);
+  if (out_fp32) return AEISU_FUSED(_Float16, float);
+  return AEISU_FUSED(_Float16, _Float16);
+#undef AEISU_FUSED
 }
 
 }  // namespace aeisu

@@ -12,12 +12,18 @@
 //      clamp(v) = u + 0.05 w,   u = s min(|v|, 2),   w = s max(min(|v|, 12) - 2, 0),
 //    where u and w are exact FP16 values computed with packed FP16 / u16 operations
 //    (NaN coefficients keep a NaN u).  Lane (n, g) splits coefficients 4g..4g+3 of
-//    pixel n (each coefficient once per wave); two permlane swaps then give lane
-//    group g the MFMA operand slots 8g..8g+7 of B = [u(0..15) ; w(0..15)].
-//  * Synthesis on MFMA (16x16x32 f16): D[112 x 16] = Bank^T[112 x 32] . B[32 x 16], two
-//    MFMAs per row tile with FP32 accumulation, the learned base as the C operand:
-//      W = base + [K_hi | (0.05K)_hi] . B + [K_lo | (0.05K)_lo] . B
-//    (FP32 bank and 0.05 * bank split into FP16 hi + lo, ~2^-22 relative to the FP32 math).
+//    pixel n, i.e. each coefficient once per wave.
+//  * Synthesis on MFMA, two dependent 16x16x32 f16 MFMAs per row tile (FP32 accumulation),
+//    D[112 x 16] rows = (tap, phase), columns = pixels:
+//      [K_hi | K_lo] . [u ; u]             u regrouped across lane groups by two permlane
+//                                          swaps (B slots 8g..8g+7 = u[8(g&1)..+7])
+//      A23 . [w_g, (1, 1 if g = 0), 0, 0]  B slots 8g..8g+3 = the lane's own w (no exchange),
+//                                          A23 slots 8g..8g+3 = (0.05 K)_hi of coefficients
+//                                          4g..4g+3, slots 4, 5 = base_hi, base_lo
+//    W = base + K u + 0.05 K w with the FP32 bank and base kept to ~2^-22 relative; only
+//    0.05 K is rounded to FP16 (2^-12 relative on the clamp excess, which is <= 0.5 in the
+//    coefficient and present only for |a| > 2).  Both MFMAs have the same shape: a chain of
+//    different shapes through SrcC needs wait states the compiler does not insert here.
 //  * Row layout (packed on the host): tiles 0..5, row 4g+i = (tap 4t+g, phase i);
 //    tile 6, row 4g = (tap 24, phase ph(g)), other rows zero.  Accumulator lane
 //    (n, g) therefore holds W for pixel n, taps 4t+g (t < 6), all four phases:
@@ -41,7 +47,8 @@ constexpr int kHeadLW = kHeadTW + 4, kHeadLH = kHeadTH + 4;
 constexpr int kHeadLPos = kHeadLW * kHeadLH;              // RGB positions per tile (with halo)
 constexpr int kHeadFill = (kHeadLPos + 255) / 256;        // positions loaded per thread
 constexpr int kHeadChunks = kHeadTW / 16;
-constexpr int kHeadFrags = 14;                            // 7 row tiles x {hi, lo} fragments
+// bank image: 7 K=32 fragments (h8 per lane), then 7 + 7 K=16 fragments (h4 per lane)
+constexpr int kHeadFragBytes = 7 * 64 * 16 + 14 * 64 * 8;
 
 template <typename Tin>
 __device__ __forceinline__ float load_px(const Tin* p) { return (float)*p; }
@@ -131,15 +138,13 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
   __shared__ float4 tiles[2][kHeadLPos];
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  h8 A1[7], A2[7];   // [K_hi | (0.05K)_hi] and [K_lo | (0.05K)_lo] fragments
-  f4 base[7];        // learned base in accumulator layout (rows 4g..4g+3 of each tile)
-  const f4* base_src = reinterpret_cast<const f4*>(bankA + kHeadFrags * 64);
+  h8 A1[7], A23[7];  // [K_hi | K_lo] and [(0.05K)_hi of 4g..4g+3, base_hi, base_lo, 0, 0] per lane group
 #pragma unroll
   for (int t = 0; t < 7; ++t) {
     A1[t] = bankA[t * 64 + lane];
-    A2[t] = bankA[(7 + t) * 64 + lane];
-    base[t] = base_src[t * 4 + g];
+    A23[t] = bankA[(7 + t) * 64 + lane];
   }
+  const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
   // LDS offsets (float4 units, relative to the pixel's top-left tap) of taps 4t+g
   int toff[6];
 #pragma unroll
@@ -181,22 +186,25 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
       for (int j = 0; j < kHeadChunks; ++j) {
         if (t.x0 + 16 * j >= W) break;               // wave-uniform
         const int x = t.x0 + 16 * j + n;
-        // coefficients 4g..4g+3 of pixel n -> (u, w) halves, then regroup across lane groups
+        // coefficients 4g..4g+3 of pixel n -> (u, w) halves
         unsigned U[2], Wd[2];
         clamp_split(coef[j][0], U[0], Wd[0]);
         clamp_split(coef[j][1], U[1], Wd[1]);
-        // (U, W) of groups 0..3 -> group g holds slots 8g..8g+7 of [u ; w]
+        // u of groups 0..3 -> group g holds u[8(g&1) .. 8(g&1)+7]
+        unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
 #pragma unroll
-        for (int w = 0; w < 2; ++w) permlane32_swap_u(U[w], Wd[w]);
+        for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
 #pragma unroll
-        for (int w = 0; w < 2; ++w) permlane16_swap_u(U[w], Wd[w]);
-        const u4 bw = {U[0], U[1], Wd[0], Wd[1]};
-        const h8 bop = __builtin_bit_cast(h8, bw);
+        for (int w = 0; w < 2; ++w) permlane16_swap_mfma(Ux[w], Uy[w]);
+        const u4 bu = {Ux[0], Ux[1], Uy[0], Uy[1]};
+        const u4 bw = {Wd[0], Wd[1], ones, 0u};
+        const h8 bop_u = __builtin_bit_cast(h8, bu);
+        const h8 bop_w = __builtin_bit_cast(h8, bw);
         f4 acc[7];
 #pragma unroll
         for (int r = 0; r < 7; ++r) {
-          acc[r] = mfma_f16(A1[r], bop, base[r]);
-          acc[r] = mfma_f16(A2[r], bop, acc[r]);
+          acc[r] = mfma_f16(A1[r], bop_u, f4{0.f, 0.f, 0.f, 0.f});
+          acc[r] = mfma_f16(A23[r], bop_w, acc[r]);
         }
         const float4* L0 = buf + wave * kHeadLW + 16 * j + n;
         float o[12];

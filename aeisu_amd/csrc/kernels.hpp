@@ -26,8 +26,9 @@ hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* m
                        void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
                        unsigned* nonfinite, int grid, hipStream_t stream);
 
-// Fused refine + tail + head (coefficients in LDS); one 768-thread block per CU.
-int fused_num_tiles(int batch, int H, int W, int Hq, int Wq, int py, int px);
+// Fused refine + tail + head (coefficients in LDS); one block per CU (1024 threads for FP16
+// frames, 768 for FP32 frames).
+int fused_num_tiles(int in_fp32, int batch, int H, int W, int Hq, int Wq, int py, int px);
 hipError_t fused_prepare();
 hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, const void* work, const void* src, const void* rt_frag,
                                   const float* rbias, const float* tbias, const void* bankA, void* out, int H, int W,

@@ -74,7 +74,10 @@ def test_head_matches_oracle_reconstruction(fp16_model, area_state, scale):
     got = fp16_model.head(src[None].cuda().contiguous(), meta_nhwc, out_dtype=torch.float32).cpu()
     err = (got - ref).abs().max().item()
     say(f"  max|gpu-oracle| = {err:.3g}")
-    assert err < 2e-5
+    # W = base + K u + 0.05 K w: base and bank are kept to ~2^-22, only 0.05 K is an FP16 value, so a
+    # clamped coefficient (excess w <= 10) adds <= 2^-12 * 0.05 |K| w to a tap weight.  Measured on this
+    # frame: 2.6e-5 at scale 1, 8.7e-5 at scale 3 (most coefficients clamped).
+    assert err < 1.5e-4
 
 
 def test_head_phase_packing_exact(fp16_model, area_state):
