@@ -276,7 +276,8 @@ struct Runtime {
   DeviceBuffer skip, work, meta, nonfinite;
   DeviceBuffer low[5];
   int nlow = 2;
-  bool fused = false;              // refine + tail + head in one kernel (coefficients on chip)
+  bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
+                                   // (body activations and coefficients stay on chip)
   bool fused_ready = false;        // fused kernels' LDS limit raised on this device
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
   // captured frame graphs, one per (input, output) buffer pair (a small LRU-free cache)
@@ -575,7 +576,9 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   // the coefficient tensor only exists in device memory on the unfused path
   if (flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED)) rt.meta.alloc(packed * 64 * 2);
   else rt.meta.release();
-  rt.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : 2;
+  // low-resolution activations only reach device memory on the per-layer path
+  const bool fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
+  rt.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : (fused ? 0 : 2);
   for (int i = 0; i < 5; ++i) {
     if (i < rt.nlow) rt.low[i].alloc(lowpx * 64 * rt.low_elem());
     else rt.low[i].release();
@@ -590,10 +593,11 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, m), cus);
   rt.grid.refine = clamp_grid(refine_num_tiles(batch, rt.Hq, rt.Wq), refine_blocks_per_cu(), cus);
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
-  rt.fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
+  rt.fused = fused;
   rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
+    check_hip(body_fused_prepare(), "hipFuncSetAttribute(fused body LDS)");
     rt.fused_ready = true;
   }
   rt.configured = true;
@@ -612,6 +616,29 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
                            rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.grid.project, s), "project launch");
   if (ev) check_hip(hipEventRecord(ev[1], s), "hipEventRecord");
   const float* A = rt.act;
+  if (rt.fused) {
+    // one kernel for compress .. expand: the compress and expand stages read zero and the
+    // bottleneck stage times the whole body
+    if (ev) check_hip(hipEventRecord(ev[2], s), "hipEventRecord");
+    BodyFusedArgs P{};
+    P.skip = static_cast<const _Float16*>(rt.skip.ptr);
+    P.work = static_cast<_Float16*>(rt.work.ptr);
+    const LayerDev* layers[6] = {&rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3], &rt.expand};
+    for (int l = 0; l < 6; ++l) {
+      P.frag[l] = layers[l]->frag.ptr;
+      P.bias[l] = layers[l]->bias.as<float>();
+      P.scale[l] = m ? layers[l]->scale.as<float>() : nullptr;
+      P.inv_out[l] = m ? inv(A[l + 2]) : 0.f;   // compress s2, bottleneck i s(i+3), expand s7
+    }
+    P.inv_in = m ? inv(A[1]) : 0.f;
+    P.s_out = m ? A[7] : 0.f;
+    P.Hl = rt.Hl;
+    P.Wl = rt.Wl;
+    check_hip(launch_body_fused(m, P, rt.batch, s), "fused body launch");
+    if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
+    if (ev) check_hip(hipEventRecord(ev[4], s), "hipEventRecord");
+    return;
+  }
   check_hip(launch_compress(m, rt.skip.ptr, rt.compress.frag.ptr, rt.compress.bias.as<float>(),
                             rt.compress.scale.as<float>(), rt.low[low_slot(rt, 0)].ptr, m ? inv(A[1]) : 0.f,
                             m ? inv(A[2]) : 0.f, rt.Hl, rt.Wl, rt.batch, rt.grid.compress, s), "compress launch");
@@ -883,6 +910,9 @@ int aeisu_copy_intermediate(aeisu_runtime* h, int which, void* d_dst, size_t byt
       src = rt.meta.ptr;
     } else {
       const int li = which - AEISU_BUF_LOW0;
+      if (rt.nlow == 0)
+        aeisu::fail(AEISU_ERR_STATE, "the fused body keeps activations on chip; configure with "
+                                     "AEISU_FLAG_UNFUSED or AEISU_FLAG_KEEP_INTERMEDIATES to read them");
       if (rt.nlow != 5 && li != 4) aeisu::fail(AEISU_ERR_STATE, "configure with AEISU_FLAG_KEEP_INTERMEDIATES to read this layer");
       src = rt.low[aeisu::low_slot(rt, li)].ptr;
     }

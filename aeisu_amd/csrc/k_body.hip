@@ -105,10 +105,10 @@ __global__ __launch_bounds__(256) void compress_kernel(
       for (int k = 0; k < 4; ++k) {
         const u4 raw = *reinterpret_cast<const u4*>(
             skip + (((size_t)b * Hq + 2 * ly + (k >> 1)) * Wq + 2 * lxc + (k & 1)) * 32 + 8 * g);
-        const unsigned lo = pack_e4m3x4(h2f_lo(raw[0]) * inv_in, h2f_hi(raw[0]) * inv_in,
-                                        h2f_lo(raw[1]) * inv_in, h2f_hi(raw[1]) * inv_in);
-        const unsigned hi = pack_e4m3x4(h2f_lo(raw[2]) * inv_in, h2f_hi(raw[2]) * inv_in,
-                                        h2f_lo(raw[3]) * inv_in, h2f_hi(raw[3]) * inv_in);
+        const unsigned lo = pack_e4m3x4(h2f_lo_mul(raw[0], inv_in), h2f_hi_mul(raw[0], inv_in),
+                                        h2f_lo_mul(raw[1], inv_in), h2f_hi_mul(raw[1], inv_in));
+        const unsigned hi = pack_e4m3x4(h2f_lo_mul(raw[2], inv_in), h2f_hi_mul(raw[2], inv_in),
+                                        h2f_lo_mul(raw[3], inv_in), h2f_hi_mul(raw[3], inv_in));
         if constexpr (MODE == 1) {
           const long bop = (long)(((unsigned long)hi << 32) | lo);
 #pragma unroll

@@ -26,6 +26,23 @@ hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* m
                        void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
                        unsigned* nonfinite, int grid, hipStream_t stream);
 
+// Fused body: compress, the four grouped layers and expand in one kernel (activations in LDS).
+// Layer order in the arrays: 0 compress, 1..4 bottleneck 0..3, 5 expand.
+struct BodyFusedArgs {
+  const _Float16* skip;
+  _Float16* work;
+  const void* frag[6];
+  const float* bias[6];
+  const float* scale[6];   // per-channel dequantization (null for the FP16 policy)
+  float inv_out[6];        // 1 / output activation scale of each layer (quantized policies)
+  float inv_in;            // 1 / compress input scale
+  float s_out;             // expand output scale (dequantization before the skip add)
+  int Hl, Wl;
+};
+int body_fused_num_tiles(int mode, int batch, int Hl, int Wl);
+hipError_t body_fused_prepare();
+hipError_t launch_body_fused(int mode, const BodyFusedArgs& args, int batch, hipStream_t stream);
+
 // Fused refine + tail + head (coefficients in LDS); one block per CU (1024 threads for FP16
 // frames, 768 for FP32 frames).
 int fused_num_tiles(int in_fp32, int batch, int H, int W, int Hq, int Wq, int py, int px);

@@ -54,6 +54,11 @@ def int8_model(R):
     return R.load_model(WEIGHTS / "aeisu_int8_fp16.pt", precision="int8")
 
 
+@pytest.fixture(scope="module")
+def fp8mma_model(R):
+    return R.load_model(WEIGHTS / "aeisu_area_mixed_fp8.bin", precision="mixed-fp8mma")
+
+
 def _frame(h, w, seed, texture=True):
     from aeisu_amd import frames
     return frames.scene(h, w, seed, shapes=6, texture=texture)
@@ -99,18 +104,20 @@ def test_head_phase_packing_exact(fp16_model, area_state):
 
 
 # ------------------------------------------------------------------------------------------------
-# fused refine + tail + head (coefficients on chip) vs the two-kernel path
+# fused kernels (body activations and coefficients on chip) vs the per-layer path
 # ------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("h,w,b,fp32", [(72, 104, 1, False), (70, 102, 2, True), (37, 333, 1, False),
-                                         (540, 960, 1, False)])
-def test_fused_equals_unfused(mixed_model, fp16_model, h, w, b, fp32):
-    """Same arithmetic, same rounding points: the fused kernel must reproduce the two-kernel path bit for bit,
-    including odd padding offsets (70x102 -> py = px = 29) and frames narrower than one tile row."""
+                                         (540, 960, 1, False), (200, 72, 3, False)])
+def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model, h, w, b, fp32):
+    """Same arithmetic, same rounding points: the fused body kernel and the fused refine+tail+head kernel
+    must reproduce the per-layer path bit for bit in every policy, including odd padding offsets
+    (70x102 -> py = px = 29), frames narrower than one tile row and low grids that are not a multiple
+    of the body tile (37x333, 200x72 in a batch of 3)."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
     frames = torch.stack([_frame(h, w, 40 + i) for i in range(b)]).to(dt).cuda().contiguous()
-    for model in (mixed_model, fp16_model):
+    for model in (mixed_model, fp16_model, int8_model, fp8mma_model):
         fused = model.run(frames)
         unfused = model.run(frames, flags=L.FLAG_UNFUSED)
         torch.cuda.synchronize()
