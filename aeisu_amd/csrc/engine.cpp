@@ -268,6 +268,7 @@ struct Runtime {
   float act[10] = {};
   LayerDev project, compress, grouped[4], expand, refine_tail, head;
   DeviceBuffer tail_bias;
+  DeviceBuffer body_consts;        // epilogue constants of the fused body (kBodyConsts floats)
   // geometry
   bool configured = false;
   int batch = 0, H = 0, W = 0, Hp = 0, Wp = 0, py = 0, px = 0, Hq = 0, Wq = 0, Hl = 0, Wl = 0;
@@ -478,6 +479,28 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
     }
   }
 
+  // --- fused-body epilogue constants (layout: kBodyConsts in kernels.hpp), from the staged images
+  {
+    auto staged_f32 = [](const DeviceBuffer& d, size_t i) {
+      float v = 0.f;
+      if (!d.staged.empty()) std::memcpy(&v, d.staged.data() + 4 * i, 4);
+      return v;
+    };
+    std::vector<float> cst(kBodyConsts, 0.f);
+    const LayerDev* body[5] = {&rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3]};
+    for (int l = 0; l < 5; ++l)
+      for (int c = 0; c < 64; ++c) {
+        cst[128 * l + c] = staged_f32(body[l]->bias, c);
+        cst[128 * l + 64 + c] = rt.mode ? staged_f32(body[l]->scale, c) : 0.f;
+      }
+    for (int j = 0; j < 128; ++j) {
+      const int T = j >> 4, mm = j & 15, o = (16 * (T >> 2) + mm) * 4 + (T & 3);
+      cst[640 + j] = staged_f32(rt.expand.bias, o);
+      cst[768 + j] = rt.mode ? staged_f32(rt.expand.scale, o) : 0.f;
+    }
+    rt.body_consts.upload(cst);
+  }
+
   // --- head bank: two K=32 fragment sets of 7 row tiles each, FP32 accumulation in the kernel:
   //   A1  = [K_hi | K_lo]                         against [u ; u]
   //   A23 = slots 8g..8g+3: (0.05 K)_hi of coefficients 4g..4g+3, slots 4, 5: base_hi, base_lo
@@ -526,6 +549,7 @@ static void commit_weights(Runtime& rt) {
     l->scale.commit();
   }
   rt.tail_bias.commit();
+  rt.body_consts.commit();
 }
 
 static int clamp_grid(int tiles, int per_cu, int cus) {
@@ -623,11 +647,10 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     BodyFusedArgs P{};
     P.skip = static_cast<const _Float16*>(rt.skip.ptr);
     P.work = static_cast<_Float16*>(rt.work.ptr);
+    P.consts = rt.body_consts.as<float>();
     const LayerDev* layers[6] = {&rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3], &rt.expand};
     for (int l = 0; l < 6; ++l) {
       P.frag[l] = layers[l]->frag.ptr;
-      P.bias[l] = layers[l]->bias.as<float>();
-      P.scale[l] = m ? layers[l]->scale.as<float>() : nullptr;
       P.inv_out[l] = m ? inv(A[l + 2]) : 0.f;   // compress s2, bottleneck i s(i+3), expand s7
     }
     P.inv_in = m ? inv(A[1]) : 0.f;

@@ -28,12 +28,17 @@ hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* m
 
 // Fused body: compress, the four grouped layers and expand in one kernel (activations in LDS).
 // Layer order in the arrays: 0 compress, 1..4 bottleneck 0..3, 5 expand.
+// consts: the per-channel epilogue constants of all six layers, kBodyConsts floats:
+//   [0, 64) compress bias, [64, 128) compress scale, then per bottleneck l = 0..3
+//   [128 + 128 l, +64) bias and [+64, +128) scale, then expand [640, 768) bias and
+//   [768, 896) scale, both indexed T * 16 + m for output channel (16 * (T >> 2) + m) * 4 + (T & 3).
+//   Scales are 0 for the FP16 policy.
+constexpr int kBodyConsts = 896;
 struct BodyFusedArgs {
   const _Float16* skip;
   _Float16* work;
   const void* frag[6];
-  const float* bias[6];
-  const float* scale[6];   // per-channel dequantization (null for the FP16 policy)
+  const float* consts;
   float inv_out[6];        // 1 / output activation scale of each layer (quantized policies)
   float inv_in;            // 1 / compress input scale
   float s_out;             // expand output scale (dequantization before the skip add)
