@@ -505,20 +505,17 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
   //   A1  = [K_hi | K_lo]                         against [u ; u]
   //   A23 = slots 8g..8g+3: (0.05 K)_hi of coefficients 4g..4g+3, slots 4, 5: base_hi, base_lo
   //                                               against the lane's own w and [1, 1] (group 0)
-  // (clamp(a) = u + 0.05 w in the kernel).  Row m = 4g + i of tile t < 6 is (tap 4t + g,
-  // phase i); tile 6 row 4g is (tap 24, phase 2(g&1) + (g>>1)), the phase lane group g holds
-  // after the kernel's cross-lane reduction; the other rows of tile 6 are zero.
+  // (clamp(a) = u + 0.05 w in the kernel).  Row m = 4g + i of tile t is (phase g, tap 4t + i);
+  // taps 25..27 (tile 6, i > 0) are zero rows.  The accumulator lane (n, g) thus holds all 25
+  // taps of phase g for pixel n.
   {
     const float* K = basis.f32();  // [25][16][4]
     const float* B = base.f32();   // [25][4]
     auto row_of = [](int t, int m, int& tap, int& ph) {
       const int g = m / 4, i = m % 4;
-      tap = 4 * t + g;
-      ph = i;
-      if (t == 6) {
-        tap = i == 0 ? 24 : -1;
-        ph = ((g & 1) << 1) | (g >> 1);
-      }
+      tap = 4 * t + i;
+      ph = g;
+      if (tap > 24) tap = -1;
     };
     auto hi = [](double v) { return f32_to_f16_bits((float)v); };
     auto lo = [](double v) {

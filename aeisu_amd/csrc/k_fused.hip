@@ -256,8 +256,7 @@ __device__ __forceinline__ void fstore_pair<float>(float* p, float left, float r
 template <typename Tout, typename Rgb>
 __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const Rgb* lds_rgb, Tout* __restrict__ out,
                                             FusedTile t, const FusedGeom& G, int r, int lane, const h8 (&A1)[7],
-                                            const h8 (&A23)[7], const unsigned ones, const int (&toff)[6],
-                                            float& chk) {
+                                            const h8 (&A23)[7], const unsigned ones, float& chk) {
   const int n = lane & 15, g = lane >> 4;
   const int y = 2 * t.qy0 + r - G.py;
   if (y < 0 || y >= G.H) return;                      // wave-uniform
@@ -290,48 +289,28 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       acc[q] = mfma_f16(A23[q], bop_w, acc[q]);
     }
     const Rgb* L0 = lds_rgb + r * kFRW + 16 * j + n;
-    float o[12];
+    // phase g of pixel n: the 25 taps in order (dy, dx) = (tap / 5, tap % 5)
+    float u[3] = {0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 12; ++i) o[i] = 0.f;
-#pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      const Rgb L = L0[toff[q]];
-#pragma unroll
-      for (int ph = 0; ph < 4; ++ph) {
-        o[0 * 4 + ph] = fmaf(acc[q][ph], (float)L.x, o[0 * 4 + ph]);
-        o[1 * 4 + ph] = fmaf(acc[q][ph], (float)L.y, o[1 * 4 + ph]);
-        o[2 * 4 + ph] = fmaf(acc[q][ph], (float)L.z, o[2 * 4 + ph]);
-      }
+    for (int tap = 0; tap < 25; ++tap) {
+      const Rgb L = L0[(tap / 5) * kFRW + tap % 5];
+      const float wt = acc[tap >> 2][tap & 3];
+      u[0] = fmaf(wt, (float)L.x, u[0]);
+      u[1] = fmaf(wt, (float)L.y, u[1]);
+      u[2] = fmaf(wt, (float)L.z, u[2]);
     }
-    float s[6];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      float a = o[2 * i], z = o[2 * i + 1];
-      permlane32_swap(a, z);
-      s[i] = a + z;
-    }
-    float u[3];
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-      float a = s[2 * c], z = s[2 * c + 1];
-      permlane16_swap(a, z);
-      u[c] = a + z;
-    }
-    const Rgb L24 = L0[4 * kFRW + 4];
-    u[0] = fmaf(acc[6][0], (float)L24.x, u[0]);
-    u[1] = fmaf(acc[6][0], (float)L24.y, u[1]);
-    u[2] = fmaf(acc[6][0], (float)L24.z, u[2]);
     const bool inside = x >= 0 && x < G.W;
     chk = fmaf(inside ? u[0] + u[1] + u[2] : 0.f, 0.0f, chk);
+    // pair phases (TL, TR) in lane group 0 and (BL, BR) in lane group 2
     float left[3], right[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
       left[c] = __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f);
       right[c] = left[c];
-      permlane32_swap(left[c], right[c]);
+      permlane16_swap(left[c], right[c]);
     }
-    if (g < 2 && inside) {
-      Tout* p = ob + (size_t)(2 * y + g) * (2 * G.W) + 2 * x;
+    if ((g & 1) == 0 && inside) {
+      Tout* p = ob + (size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x;
 #pragma unroll
       for (int c = 0; c < 3; ++c) fstore_pair<Tout>(p + c * oplane, left[c], right[c]);
     }
@@ -382,18 +361,12 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
   typedef typename FusedCfg<Tin>::Rgb Rgb;
   const int g = lane >> 4;
   h8 A1[7], A23[7];
-  int toff[6];
 #pragma unroll
   for (int q = 0; q < 7; ++q) {
     A1[q] = bankA[q * 64 + lane];
     A23[q] = bankA[(7 + q) * 64 + lane];
   }
   const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
-#pragma unroll
-  for (int q = 0; q < 6; ++q) {
-    const int tap = 4 * q + g;
-    toff[q] = (tap / 5) * kFRW + tap % 5;
-  }
   float chk = 0.f;
   const int t0 = tile_of(0, G.num_tiles);
   if (t0 < G.num_tiles) {
@@ -413,7 +386,7 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
     if (tn < G.num_tiles) rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(tn, G), G, ctid);
     consume_row<Tout, Rgb>(smem + LY::OffMeta + cur * LY::SizeMeta,
                            reinterpret_cast<const Rgb*>(smem + LY::OffRgb + cur * LY::SizeRgb), out,
-                           fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, ones, toff, chk);
+                           fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, ones, chk);
     if (tn < G.num_tiles) rgb_store<Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
     __syncthreads();
   }

@@ -24,18 +24,17 @@
 //    0.05 K is rounded to FP16 (2^-12 relative on the clamp excess, which is <= 0.5 in the
 //    coefficient and present only for |a| > 2).  Both MFMAs have the same shape: a chain of
 //    different shapes through SrcC needs wait states the compiler does not insert here.
-//  * Row layout (packed on the host): tiles 0..5, row 4g+i = (tap 4t+g, phase i);
-//    tile 6, row 4g = (tap 24, phase ph(g)), other rows zero.  Accumulator lane
-//    (n, g) therefore holds W for pixel n, taps 4t+g (t < 6), all four phases:
-//    it applies those 6 taps x 4 phases x 3 channels with FP32 FMAs from an LDS
-//    RGB tile, the four lane groups are summed with permlane32/16 swaps, after
-//    which lane group g holds phase ph(g) = 2(g&1) + (g>>1) and adds tap 24.
+//  * Row layout (packed on the host): row 4g+i of tile t = (phase g, tap 4t+i), taps
+//    25..27 zero.  Accumulator lane (n, g) therefore holds W for pixel n, phase g, all 25
+//    taps: it applies them to the 3 channels with FP32 FMAs in tap order from an LDS RGB
+//    tile (lanes of one pixel read the same LDS words), with no cross-lane reduction.
 //  * Pipelining: a block walks tiles of 64x4 LR pixels; the RGB tile (with a
 //    2-pixel clamped halo) and each lane's FP16 coefficients of the NEXT tile
 //    are loaded into registers while the current tile is computed, and the RGB
 //    tile is double-buffered in LDS (one barrier per tile).
-//  * Output: partner lanes (g, g+2) hold horizontally adjacent output pixels;
-//    one permlane32 swap pairs them, so each store writes two values.  A per-lane
+//  * Output: lane groups (0, 1) and (2, 3) hold horizontally adjacent output pixels
+//    (phases TL/TR, BL/BR); one permlane16 swap pairs them, so groups 0 and 2 each store
+//    two values per channel.  A per-lane
 //    running sum 0 * output (NaN for any non-finite output) sets the nonfinite
 //    flag once per wave at the end.
 #include "common.hpp"
@@ -145,13 +144,6 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
     A23[t] = bankA[(7 + t) * 64 + lane];
   }
   const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
-  // LDS offsets (float4 units, relative to the pixel's top-left tap) of taps 4t+g
-  int toff[6];
-#pragma unroll
-  for (int t = 0; t < 6; ++t) {
-    const int tap = 4 * t + g;
-    toff[t] = (tap / 5) * kHeadLW + tap % 5;
-  }
   float chk = 0.f;   // 0 * every output of this lane: NaN iff one was not finite
 
   const int tiles_x = (W + kHeadTW - 1) / kHeadTW, tiles_y = (H + kHeadTH - 1) / kHeadTH;
@@ -207,50 +199,27 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
           acc[r] = mfma_f16(A23[r], bop_w, acc[r]);
         }
         const float4* L0 = buf + wave * kHeadLW + 16 * j + n;
-        float o[12];
+        // phase g of pixel n: the 25 taps in order (dy, dx) = (tap / 5, tap % 5)
+        float u[3] = {0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 12; ++i) o[i] = 0.f;
-#pragma unroll
-        for (int r = 0; r < 6; ++r) {
-          const float4 L = L0[toff[r]];
-#pragma unroll
-          for (int ph = 0; ph < 4; ++ph) {
-            o[0 * 4 + ph] = fmaf(acc[r][ph], L.x, o[0 * 4 + ph]);
-            o[1 * 4 + ph] = fmaf(acc[r][ph], L.y, o[1 * 4 + ph]);
-            o[2 * 4 + ph] = fmaf(acc[r][ph], L.z, o[2 * 4 + ph]);
-          }
+        for (int tap = 0; tap < 25; ++tap) {
+          const float4 L = L0[(tap / 5) * kHeadLW + tap % 5];
+          const float wt = acc[tap >> 2][tap & 3];
+          u[0] = fmaf(wt, L.x, u[0]);
+          u[1] = fmaf(wt, L.y, u[1]);
+          u[2] = fmaf(wt, L.z, u[2]);
         }
-        // Sum the four lane groups (g = lane >> 4) holding the same pixel.
-        float s[6];
-#pragma unroll
-        for (int i = 0; i < 6; ++i) {
-          float a = o[2 * i], z = o[2 * i + 1];
-          permlane32_swap(a, z);
-          s[i] = a + z;
-        }
-        float u[3];
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-          float a = s[2 * c], z = s[2 * c + 1];
-          permlane16_swap(a, z);
-          u[c] = a + z;
-        }
-        // lane group g now holds phase ph(g) of pixel n; add tap 24 (dy = dx = 4)
-        const float4 L24 = L0[4 * kHeadLW + 4];
-        u[0] = fmaf(acc[6][0], L24.x, u[0]);
-        u[1] = fmaf(acc[6][0], L24.y, u[1]);
-        u[2] = fmaf(acc[6][0], L24.z, u[2]);
         chk = fmaf(u[0] + u[1] + u[2], 0.0f, chk);
-        // pair phase ph(g) (left column) with ph(g+2) = ph(g) + 1 (right column) in lanes 0..31
+        // pair phases (TL, TR) in lane group 0 and (BL, BR) in lane group 2
         float left[3], right[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
           left[c] = __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f);
           right[c] = left[c];
-          permlane32_swap(left[c], right[c]);
+          permlane16_swap(left[c], right[c]);
         }
-        if (g < 2 && x < W) {
-          Tout* p = ob + (size_t)(2 * y + g) * (2 * W) + 2 * x;
+        if ((g & 1) == 0 && x < W) {
+          Tout* p = ob + (size_t)(2 * y + (g >> 1)) * (2 * W) + 2 * x;
 #pragma unroll
           for (int c = 0; c < 3; ++c) store_pair<Tout>(p + c * oplane, left[c], right[c]);
         }

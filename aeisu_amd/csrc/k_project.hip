@@ -13,10 +13,12 @@
 // phase 2i+j, channel = feature*4 + phase; padded LR (Y, X) reads source
 // (clamp(Y-py), clamp(X-px)) -- the replicate padding of aeisu/runtime.py:84.
 //
-// gfx950 mapping: a block computes an 8x32 packed tile.  Luma of the
-// 18x66 LR halo region goes to LDS; each thread forms the 32 features of one
-// packed pixel into an LDS row; each wave then runs MFMAs (16x16x32 f16) per
-// 16 pixels against register-resident project weights.
+// gfx950 mapping: a block computes an 8x32 packed tile.  The RGB of the tile's
+// 18x66 LR halo region is staged in LDS with coalesced row loads (one global read
+// per source pixel per tile; the next tile's RGB is loaded into registers while the
+// current one is computed), luma of the halo goes to LDS, each thread forms the 32
+// features of one packed pixel into an LDS row, and each wave then runs MFMAs
+// (16x16x32 f16) per 16 pixels against register-resident project weights.
 //
 // Two precisions:
 //  * PRECISE = false (Mixed / INT8 policies): features and weights rounded to
@@ -36,13 +38,8 @@ struct Analysis {
 
 constexpr int kPTW = 32, kPTH = 8;
 constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
-constexpr int kPFeat = 72;  // halves per LDS feature row: 32 hi + 32 lo + 8 pad
-
-template <typename Tin>
-__device__ __forceinline__ float3 rgb_at(const Tin* s, size_t plane, int W, int y, int x) {
-  const size_t o = (size_t)y * W + x;
-  return make_float3((float)s[o], (float)s[plane + o], (float)s[2 * plane + o]);
-}
+// halves per LDS feature row: 32 features (+ 32 low parts in the FP32-accurate variant) + 8 pad
+template <bool PRECISE> constexpr int kPFeat = PRECISE ? 72 : 40;
 
 __device__ __forceinline__ float dot3_unfused(float3 v, float a, float b, float c) {
   return __fadd_rn(__fadd_rn(__fmul_rn(v.x, a), __fmul_rn(v.y, b)), __fmul_rn(v.z, c));
@@ -52,12 +49,42 @@ __device__ __forceinline__ float comb3(float p, float a, float q, float b, float
   return __fadd_rn(__fadd_rn(__fmul_rn(p, a), __fmul_rn(q, b)), __fmul_rn(r, c));
 }
 
+constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
+constexpr int kPStage = (3 * kPRgb + 255) / 256;         // staged RGB values per thread
+
+template <typename Tin>
+struct ProjectStage {
+  float v[kPStage];
+};
+// RGB of the halo region of tile tidx (padded LR origin (Y0, X0)), clamped to the source
+// (replicate padding), planar [c][r][col]; element i of the stage is region value
+// tid + 256 i.
+template <typename Tin>
+__device__ __forceinline__ void project_fetch(ProjectStage<Tin>& st, const Tin* __restrict__ src, int b, int Y0,
+                                              int X0, int H, int W, int py, int px, int tid) {
+  const size_t plane = (size_t)H * W;
+  const Tin* s = src + (size_t)b * 3 * plane;
+#pragma unroll
+  for (int i = 0; i < kPStage; ++i) {
+    const int q = tid + 256 * i;
+    float v = 0.f;
+    if (q < 3 * kPRgb) {
+      const int c = q / kPRgb, rem = q - c * kPRgb;
+      const int r = rem / kPLW, col = rem - r * kPLW;
+      const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + col - px, 0), W - 1);
+      v = (float)s[c * plane + (size_t)sy * W + sx];
+    }
+    st.v[i] = v;
+  }
+}
+
 template <typename Tin, bool PRECISE>
 __global__ __launch_bounds__(256) void project_kernel(
     const Tin* __restrict__ src, const h8* __restrict__ wfrag, const float* __restrict__ bias,
     _Float16* __restrict__ skip, Analysis an, int H, int W, int Hq, int Wq, int py, int px, int batch) {
+  __shared__ float rgb[3][kPLH][kPLW];
   __shared__ float luma[kPLH][kPLW + 1];
-  __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat];
+  __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat<PRECISE>];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const h8 A0 = wfrag[lane], A1 = wfrag[64 + lane];
@@ -71,23 +98,48 @@ __global__ __launch_bounds__(256) void project_kernel(
   for (int T = 0; T < 2; ++T)
 #pragma unroll
     for (int r = 0; r < 4; ++r) bs[T][r] = bias[16 * T + 4 * g + r];
-  const size_t plane = (size_t)H * W;
   const int tiles_x = (Wq + kPTW - 1) / kPTW, tiles_y = (Hq + kPTH - 1) / kPTH;
   const int num_tiles = batch * tiles_x * tiles_y;
   const int iters = tile_iters(num_tiles);
+  auto origin = [&](int tidx, int& b, int& qy0, int& qx0) {
+    b = tidx / (tiles_x * tiles_y);
+    const int rem = tidx - b * tiles_x * tiles_y;
+    qy0 = (rem / tiles_x) * kPTH;
+    qx0 = (rem % tiles_x) * kPTW;
+  };
+  ProjectStage<Tin> st;
+  {
+    const int t0 = tile_of(0, num_tiles);
+    if (t0 < num_tiles) {
+      int b, qy0, qx0;
+      origin(t0, b, qy0, qx0);
+      project_fetch<Tin>(st, src, b, 2 * qy0 - 1, 2 * qx0 - 1, H, W, py, px, tid);
+    }
+  }
   for (int it = 0; it < iters; ++it) {
     const int tidx = tile_of(it, num_tiles);
     if (tidx >= num_tiles) break;
-    const int b = tidx / (tiles_x * tiles_y);
-    const int rem = tidx - b * tiles_x * tiles_y;
-    const int qy0 = (rem / tiles_x) * kPTH, qx0 = (rem % tiles_x) * kPTW;
-    const Tin* s = src + (size_t)b * 3 * plane;
-    const int Y0 = 2 * qy0 - 1, X0 = 2 * qx0 - 1;   // padded LR origin of the luma halo
+    int b, qy0, qx0;
+    origin(tidx, b, qy0, qx0);
+    __syncthreads();                                    // previous tile's LDS reads done
+#pragma unroll
+    for (int i = 0; i < kPStage; ++i) {
+      const int q = tid + 256 * i;
+      if (q < 3 * kPRgb) (&rgb[0][0][0])[q] = st.v[i];
+    }
+    {
+      const int tn = tile_of(it + 1, num_tiles);      // next tile's RGB in flight during this one
+      if (tn < num_tiles) {
+        int bn, qyn, qxn;
+        origin(tn, bn, qyn, qxn);
+        project_fetch<Tin>(st, src, bn, 2 * qyn - 1, 2 * qxn - 1, H, W, py, px, tid);
+      }
+    }
     __syncthreads();
-    for (int q = tid; q < kPLH * kPLW; q += 256) {
+    for (int q = tid; q < kPRgb; q += 256) {
       const int r = q / kPLW, c = q - r * kPLW;
-      const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + c - px, 0), W - 1);
-      luma[r][c] = dot3_unfused(rgb_at(s, plane, W, sy, sx), an.mix[0], an.mix[1], an.mix[2]);
+      luma[r][c] = dot3_unfused(make_float3(rgb[0][r][c], rgb[1][r][c], rgb[2][r][c]), an.mix[0], an.mix[1],
+                                an.mix[2]);
     }
     __syncthreads();
     {
@@ -96,13 +148,11 @@ __global__ __launch_bounds__(256) void project_kernel(
 #pragma unroll
       for (int ph = 0; ph < 4; ++ph) {
         const int i = ph >> 1, j = ph & 1;
-        const int Y = 2 * (qy0 + ty) + i, X = 2 * (qx0 + tx) + j;
-        const int sy = min(max(Y - py, 0), H - 1), sx = min(max(X - px, 0), W - 1);
-        const float3 v = rgb_at(s, plane, W, sy, sx);
+        const int r = 2 * ty + i + 1, c = 2 * tx + j + 1;   // centre in the halo region
+        const float3 v = make_float3(rgb[0][r][c], rgb[1][r][c], rgb[2][r][c]);
         f[0][ph] = dot3_unfused(v, an.basis[0], an.basis[1], an.basis[2]);
         f[1][ph] = dot3_unfused(v, an.basis[3], an.basis[4], an.basis[5]);
         f[2][ph] = dot3_unfused(v, an.basis[6], an.basis[7], an.basis[8]);
-        const int r = 2 * ty + i + 1, c = 2 * tx + j + 1;   // centre in the luma tile
         const float ul = luma[r - 1][c - 1], uc = luma[r - 1][c], ur = luma[r - 1][c + 1];
         const float cl = luma[r][c - 1], cc = luma[r][c], cr = luma[r][c + 1];
         const float dl = luma[r + 1][c - 1], dc = luma[r + 1][c], dr = luma[r + 1][c + 1];
