@@ -73,6 +73,14 @@ __device__ __forceinline__ void permlane16_swap_mfma(unsigned& x, unsigned& y) {
 // non-negative v gives v >= v * slope, and -0 * slope = -0; two VALU ops instead of three.
 __device__ __forceinline__ float leaky(float v, float slope) { return __builtin_fmaxf(v, v * slope); }
 
+// Workgroup barrier for data handed over through LDS: waits for this wave's LDS operations
+// only.  __syncthreads() also waits for every outstanding global load and store (on gfx9
+// vmcnt counts both), which would drain prefetches issued just before it and stall each
+// tile on the write acknowledgements of its output.  The memory clobber keeps the compiler
+// from moving LDS accesses across the barrier.  Global data that feeds LDS stores is waited
+// for at those stores (register dependency), before the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // float -> OCP E4M3 with round-to-nearest-even and saturation to +-448.
 // The hardware convert rounds to nearest even but yields NaN above the
 // saturation threshold, so the value is clamped first.

@@ -71,11 +71,6 @@ __device__ __forceinline__ FragSet<MODE, N> load_frags(const void* base, int fir
   return r;
 }
 
-// Workgroup barrier for LDS hand-over: waits for this wave's LDS operations only, so global
-// loads issued before it (the next layer's weights, prefetched operands) stay in flight.  The
-// memory clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // ---- operand and epilogue helpers ---------------------------------------------------------------
 template <int MODE>
 __device__ __forceinline__ typename BodyFusedCfg<MODE>::Acc mma(typename BodyFusedCfg<MODE>::Frag a,

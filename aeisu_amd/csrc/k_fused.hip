@@ -187,35 +187,36 @@ __device__ __forceinline__ void produce(const unsigned char* smem, const unsigne
 }
 
 // ---- consumer side ----------------------------------------------------------------------------
-template <typename LY>
+// The RGB tile of the next tile is loaded into registers as raw frame values and converted
+// only when it is stored to LDS: converting at load time makes the compiler wait for each
+// load right away, which would expose the memory latency instead of hiding it behind the
+// current tile.  Loads are unconditional (indices clamped into the tile) so they are not
+// split into branches either.
+template <typename Tin, typename LY>
 struct RgbRegs {
-  float v[LY::RgbPer][3];
+  Tin v[LY::RgbPer][3];
 };
 template <typename Tin, typename LY>
-__device__ __forceinline__ void rgb_fetch(RgbRegs<LY>& r, const Tin* __restrict__ src, FusedTile t,
+__device__ __forceinline__ void rgb_fetch(RgbRegs<Tin, LY>& r, const Tin* __restrict__ src, FusedTile t,
                                           const FusedGeom& G, int ctid) {
   const size_t plane = (size_t)G.H * G.W;
   const Tin* s = src + (size_t)t.b * 3 * plane;
   const int y0 = 2 * t.qy0 - G.py - 2, x0 = 2 * t.qx0 - G.px - 2;
 #pragma unroll
   for (int k = 0; k < LY::RgbPer; ++k) {
-    const int q = ctid + LY::ConsumerThreads * k;
-    if (q < LY::RPos) {
-      const int ly = q / kFRW, lx = q - ly * kFRW;
-      const int sy = min(max(y0 + ly, 0), G.H - 1), sx = min(max(x0 + lx, 0), G.W - 1);
-      const size_t o = (size_t)sy * G.W + sx;
-      r.v[k][0] = (float)s[o];
-      r.v[k][1] = (float)s[plane + o];
-      r.v[k][2] = (float)s[2 * plane + o];
-    }
+    const int q = min(ctid + LY::ConsumerThreads * k, LY::RPos - 1);
+    const int ly = q / kFRW, lx = q - ly * kFRW;
+    const int sy = min(max(y0 + ly, 0), G.H - 1), sx = min(max(x0 + lx, 0), G.W - 1);
+    const size_t o = (size_t)sy * G.W + sx;
+    r.v[k][0] = s[o];
+    r.v[k][1] = s[plane + o];
+    r.v[k][2] = s[2 * plane + o];
   }
 }
-__device__ __forceinline__ void rgb_put(h4* d, float a, float b, float c) {
-  *d = h4{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)0.0f};   // exact: the values came from FP16
-}
+__device__ __forceinline__ void rgb_put(h4* d, _Float16 a, _Float16 b, _Float16 c) { *d = h4{a, b, c, (_Float16)0.0f}; }
 __device__ __forceinline__ void rgb_put(float4* d, float a, float b, float c) { *d = make_float4(a, b, c, 0.f); }
-template <typename Rgb, typename LY>
-__device__ __forceinline__ void rgb_store(const RgbRegs<LY>& r, Rgb* lds_rgb, int ctid) {
+template <typename Tin, typename Rgb, typename LY>
+__device__ __forceinline__ void rgb_store(const RgbRegs<Tin, LY>& r, Rgb* lds_rgb, int ctid) {
 #pragma unroll
   for (int k = 0; k < LY::RgbPer; ++k) {
     const int q = ctid + LY::ConsumerThreads * k;
@@ -241,18 +242,29 @@ __device__ __forceinline__ void fused_clamp_split(unsigned v, unsigned& u, unsig
   w = (__builtin_bit_cast(unsigned, e) & 0x7FFF7FFFu) | (v & 0x80008000u);
 }
 
+// Output stores through a raw buffer resource covering one frame: lanes whose pixel lies
+// outside the frame get an offset past the range and the hardware drops their store, so
+// the stores need no branch (raw-buffer range checking: offset >= num_records is not
+// written).  A frame is at most 3 x 8192^2 x 4 x 4 bytes < 2^32.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t frame_rsrc(void* base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(unsigned)bytes, 0x00020000);
+}
 template <typename Tout>
-__device__ __forceinline__ void fstore_pair(Tout* p, float left, float right);
+__device__ __forceinline__ void fstore_pair(__amdgpu_buffer_rsrc_t r, unsigned off, float left, float right);
 template <>
-__device__ __forceinline__ void fstore_pair<_Float16>(_Float16* p, float left, float right) {
-  *reinterpret_cast<unsigned*>(p) = pack_h2(left, right);
+__device__ __forceinline__ void fstore_pair<_Float16>(__amdgpu_buffer_rsrc_t r, unsigned off, float left, float right) {
+  __builtin_amdgcn_raw_buffer_store_b32(pack_h2(left, right), r, (int)off, 0, 0);
 }
 template <>
-__device__ __forceinline__ void fstore_pair<float>(float* p, float left, float right) {
-  *reinterpret_cast<float2*>(p) = make_float2(left, right);
+__device__ __forceinline__ void fstore_pair<float>(__amdgpu_buffer_rsrc_t r, unsigned off, float left, float right) {
+  typedef unsigned v2u __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(v2u{__builtin_bit_cast(unsigned, left), __builtin_bit_cast(unsigned, right)},
+                                        r, (int)off, 0, 0);
 }
 
-// Head on LR row `r` of the tile.
+// Head on LR row `r` of the tile.  The four 16-pixel chunks are computed unconditionally
+// (every LDS address stays inside the tile buffers), so the row is one basic block the
+// scheduler can interleave; chunks or lanes past the frame edge only lose their stores.
 template <typename Tout, typename Rgb>
 __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const Rgb* lds_rgb, Tout* __restrict__ out,
                                             FusedTile t, const FusedGeom& G, int r, int lane, const h8 (&A1)[7],
@@ -261,14 +273,12 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
   const int y = 2 * t.qy0 + r - G.py;
   if (y < 0 || y >= G.H) return;                      // wave-uniform
   const size_t oplane = (size_t)4 * G.H * G.W;
-  Tout* ob = out + (size_t)t.b * 3 * oplane;
+  const __amdgpu_buffer_rsrc_t ob = frame_rsrc(out + (size_t)t.b * 3 * oplane, 3 * oplane * sizeof(Tout));
   const _Float16* mrow = reinterpret_cast<const _Float16*>(lds_meta) + (r >> 1) * kFQW * kFMPix;
   const int rho_y = (r & 1) << 1;
 #pragma unroll
   for (int j = 0; j < kFLW / 16; ++j) {
-    const int xs = 2 * t.qx0 + 16 * j - G.px;         // LR column of lane n = 0
-    if (xs + 15 < 0 || xs >= G.W) continue;           // wave-uniform
-    const int x = xs + n;
+    const int x = 2 * t.qx0 + 16 * j - G.px + n;
     const u2 coef = *reinterpret_cast<const u2*>(mrow + (8 * j + (n >> 1)) * kFMPix + 16 * (rho_y | (n & 1)) + 4 * g);
     unsigned U[2], Wd[2];
     fused_clamp_split(coef[0], U[0], Wd[0]);
@@ -299,9 +309,10 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       u[1] = fmaf(wt, (float)L.y, u[1]);
       u[2] = fmaf(wt, (float)L.z, u[2]);
     }
-    const bool inside = x >= 0 && x < G.W;
+    const bool inside = (unsigned)x < (unsigned)G.W;
     chk = fmaf(inside ? u[0] + u[1] + u[2] : 0.f, 0.0f, chk);
-    // pair phases (TL, TR) in lane group 0 and (BL, BR) in lane group 2
+    // pair phases (TL, TR) and (BL, BR): after the swap lane groups 0 and 1 both hold
+    // (TL, TR), groups 2 and 3 both hold (BL, BR), and each pair is stored by both groups
     float left[3], right[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
@@ -309,11 +320,10 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       right[c] = left[c];
       permlane16_swap(left[c], right[c]);
     }
-    if ((g & 1) == 0 && inside) {
-      Tout* p = ob + (size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x;
+    const unsigned o0 = (unsigned)(((size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x) * sizeof(Tout));
 #pragma unroll
-      for (int c = 0; c < 3; ++c) fstore_pair<Tout>(p + c * oplane, left[c], right[c]);
-    }
+    for (int c = 0; c < 3; ++c)
+      fstore_pair<Tout>(ob, inside ? o0 + (unsigned)(c * oplane * sizeof(Tout)) : 0xFFFFFFFFu, left[c], right[c]);
   }
 }
 
@@ -334,9 +344,9 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
       patch_store<LY>(pr, smem + LY::OffPatch + LY::SizePatch, ptid);
     }
   }
-  __syncthreads();                                   // weights, biases and prologue loads visible
+  lds_barrier();                                   // weights, biases and prologue loads visible
   if (t0 < G.num_tiles) produce<LY>(smem, smem + LY::OffPatch, smem + LY::OffMeta, wave, lane);
-  __syncthreads();                                   // coefficients of tile 0 visible
+  lds_barrier();                                   // coefficients of tile 0 visible
   const int iters = tile_iters(G.num_tiles);
   for (int it = 0; it < iters; ++it) {
     if (tile_of(it, G.num_tiles) >= G.num_tiles) break;   // block-uniform, as in consumer_main
@@ -347,7 +357,7 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
     if (tn < G.num_tiles)
       produce<LY>(smem, smem + LY::OffPatch + nxt * LY::SizePatch, smem + LY::OffMeta + nxt * LY::SizeMeta, wave, lane);
     if (tnn < G.num_tiles) patch_store<LY>(pr, smem + LY::OffPatch + cur * LY::SizePatch, ptid);
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -370,25 +380,25 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
   float chk = 0.f;
   const int t0 = tile_of(0, G.num_tiles);
   if (t0 < G.num_tiles) {
-    RgbRegs<LY> rr;
+    RgbRegs<Tin, LY> rr;
     rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(t0, G), G, ctid);
-    rgb_store<Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb), ctid);
+    rgb_store<Tin, Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb), ctid);
   }
-  __syncthreads();                                   // prologue loads visible
-  __syncthreads();                                   // coefficients of tile 0 visible
+  lds_barrier();                                   // prologue loads visible
+  lds_barrier();                                   // coefficients of tile 0 visible
   const int iters = tile_iters(G.num_tiles);
   for (int it = 0; it < iters; ++it) {
     const int tc = tile_of(it, G.num_tiles);
     if (tc >= G.num_tiles) break;                    // block-uniform, as in producer_main
     const int tn = tile_of(it + 1, G.num_tiles);
     const int cur = it & 1, nxt = cur ^ 1;
-    RgbRegs<LY> rr;
+    RgbRegs<Tin, LY> rr;
     if (tn < G.num_tiles) rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(tn, G), G, ctid);
     consume_row<Tout, Rgb>(smem + LY::OffMeta + cur * LY::SizeMeta,
                            reinterpret_cast<const Rgb*>(smem + LY::OffRgb + cur * LY::SizeRgb), out,
                            fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, ones, chk);
-    if (tn < G.num_tiles) rgb_store<Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
-    __syncthreads();
+    if (tn < G.num_tiles) rgb_store<Tin, Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
+    lds_barrier();
   }
   if (nonfinite && __ballot(chk != chk) != 0ull && lane == 0) atomicOr(nonfinite, 1u);
 }

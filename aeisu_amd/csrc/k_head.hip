@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
     const int ntidx = tile_of(it + 1, num_tiles);
     if (ntidx < num_tiles)
       head_fetch(cur, src, meta, head_tile(ntidx, tiles_x, tiles_y), H, W, Hq, Wq, py, px, wave, n, g);
-    __syncthreads();                                 // buf complete; the other buffer is free again
+    lds_barrier();                                 // buf complete; the other buffer is free again
 
     const int y = t.y0 + wave;
     if (y < H) {                                     // wave-uniform

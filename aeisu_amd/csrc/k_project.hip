@@ -52,11 +52,14 @@ __device__ __forceinline__ float comb3(float p, float a, float q, float b, float
 constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
 constexpr int kPStage = (3 * kPRgb + 255) / 256;         // staged RGB values per thread
 
+// The halo RGB of the next tile is held as raw frame values and converted when stored to
+// LDS (converting at load time would make the compiler wait for every load on the spot);
+// the loads are unconditional with the index clamped into the region.
 template <typename Tin>
 struct ProjectStage {
-  float v[kPStage];
+  Tin v[kPStage];
 };
-// RGB of the halo region of tile tidx (padded LR origin (Y0, X0)), clamped to the source
+// RGB of the halo region of a tile (padded LR origin (Y0, X0)), clamped to the source
 // (replicate padding), planar [c][r][col]; element i of the stage is region value
 // tid + 256 i.
 template <typename Tin>
@@ -66,15 +69,11 @@ __device__ __forceinline__ void project_fetch(ProjectStage<Tin>& st, const Tin* 
   const Tin* s = src + (size_t)b * 3 * plane;
 #pragma unroll
   for (int i = 0; i < kPStage; ++i) {
-    const int q = tid + 256 * i;
-    float v = 0.f;
-    if (q < 3 * kPRgb) {
-      const int c = q / kPRgb, rem = q - c * kPRgb;
-      const int r = rem / kPLW, col = rem - r * kPLW;
-      const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + col - px, 0), W - 1);
-      v = (float)s[c * plane + (size_t)sy * W + sx];
-    }
-    st.v[i] = v;
+    const int q = min(tid + 256 * i, 3 * kPRgb - 1);
+    const int c = q / kPRgb, rem = q - c * kPRgb;
+    const int r = rem / kPLW, col = rem - r * kPLW;
+    const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + col - px, 0), W - 1);
+    st.v[i] = s[c * plane + (size_t)sy * W + sx];
   }
 }
 
@@ -121,11 +120,11 @@ __global__ __launch_bounds__(256) void project_kernel(
     if (tidx >= num_tiles) break;
     int b, qy0, qx0;
     origin(tidx, b, qy0, qx0);
-    __syncthreads();                                    // previous tile's LDS reads done
+    lds_barrier();                                    // previous tile's LDS reads done
 #pragma unroll
     for (int i = 0; i < kPStage; ++i) {
       const int q = tid + 256 * i;
-      if (q < 3 * kPRgb) (&rgb[0][0][0])[q] = st.v[i];
+      if (q < 3 * kPRgb) (&rgb[0][0][0])[q] = (float)st.v[i];
     }
     {
       const int tn = tile_of(it + 1, num_tiles);      // next tile's RGB in flight during this one
@@ -135,13 +134,13 @@ __global__ __launch_bounds__(256) void project_kernel(
         project_fetch<Tin>(st, src, bn, 2 * qyn - 1, 2 * qxn - 1, H, W, py, px, tid);
       }
     }
-    __syncthreads();
+    lds_barrier();
     for (int q = tid; q < kPRgb; q += 256) {
       const int r = q / kPLW, c = q - r * kPLW;
       luma[r][c] = dot3_unfused(make_float3(rgb[0][r][c], rgb[1][r][c], rgb[2][r][c]), an.mix[0], an.mix[1],
                                 an.mix[2]);
     }
-    __syncthreads();
+    lds_barrier();
     {
       const int ty = tid / kPTW, tx = tid - ty * kPTW;
       float f[8][4];
@@ -178,7 +177,7 @@ __global__ __launch_bounds__(256) void project_kernel(
         if constexpr (PRECISE) *reinterpret_cast<h8*>(&feat[tid][32 + 8 * q]) = r;
       }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       const int p = wave * 64 + jg * 16 + n;          // pixel index inside the tile

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void refine_tail_kernel(
     u4* dst = reinterpret_cast<u4*>(smem);
     for (int i = threadIdx.x; i < kRefineFrag + kTailFrag; i += 256) dst[i] = srcw[i];
   }
-  __syncthreads();
+  lds_barrier();
   h8 Ar[4][9], At[4][2];
   {
     const h8* s = reinterpret_cast<const h8*>(smem);
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void refine_tail_kernel(
     const int rem = tidx - b * tiles_x * tiles_y;
     const int y0 = (rem / tiles_x) * kRTH, x0 = (rem % tiles_x) * kRTW;
     const _Float16* in = work + (size_t)b * Hq * Wq * 32;
-    __syncthreads();
+    lds_barrier();
     for (int q = threadIdx.x; q < kRPH * kRPW * 4; q += 256) {
       const int pix = q >> 2, ch = (q & 3) * 8;
       const int ly = pix / kRPW, lx = pix - ly * kRPW;
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(256) void refine_tail_kernel(
         v = *reinterpret_cast<const u4*>(in + ((size_t)gy * Wq + gx) * 32 + ch);
       *reinterpret_cast<u4*>(&patch[ly][lx][ch]) = v;
     }
-    __syncthreads();
+    lds_barrier();
     const int yq = y0 + wave;
     if (yq >= Hq) continue;
 #pragma unroll
