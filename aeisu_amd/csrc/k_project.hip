@@ -41,12 +41,22 @@ constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
 // halves per LDS feature row: 32 features (+ 32 low parts in the FP32-accurate variant) + 8 pad
 template <bool PRECISE> constexpr int kPFeat = PRECISE ? 72 : 40;
 
+__device__ __forceinline__ float sub_rn(float a, float b) { return a - b; }
+// HIP's __fmul_rn / __fadd_rn are plain operators that the compiler may contract into FMAs
+// (-ffp-contract=fast is the default): contraction is switched off here explicitly.
 __device__ __forceinline__ float dot3_unfused(float3 v, float a, float b, float c) {
-  return __fadd_rn(__fadd_rn(__fmul_rn(v.x, a), __fmul_rn(v.y, b)), __fmul_rn(v.z, c));
+#pragma clang fp contract(off)
+  return (v.x * a + v.y * b) + v.z * c;
 }
 // (p*a + q*b) + r*c, unfused, reference order
 __device__ __forceinline__ float comb3(float p, float a, float q, float b, float r, float c) {
-  return __fadd_rn(__fadd_rn(__fmul_rn(p, a), __fmul_rn(q, b)), __fmul_rn(r, c));
+#pragma clang fp contract(off)
+  return (p * a + q * b) + r * c;
+}
+// (u - d) * a0 - m * a1 + h * a2, evaluated left to right, unfused
+__device__ __forceinline__ float d135_unfused(float u, float d, float m, float h, float a0, float a1, float a2) {
+#pragma clang fp contract(off)
+  return ((u - d) * a0 - m * a1) + h * a2;
 }
 
 constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
@@ -155,14 +165,12 @@ __global__ __launch_bounds__(256) void project_kernel(
         const float ul = luma[r - 1][c - 1], uc = luma[r - 1][c], ur = luma[r - 1][c + 1];
         const float cl = luma[r][c - 1], cc = luma[r][c], cr = luma[r][c + 1];
         const float dl = luma[r + 1][c - 1], dc = luma[r + 1][c], dr = luma[r + 1][c + 1];
-        const float hmid = __fsub_rn(cr, cl), vmid = __fsub_rn(dc, uc);
+        const float hmid = sub_rn(cr, cl), vmid = sub_rn(dc, uc);
         f[3][ph] = cc;
-        f[4][ph] = comb3(__fsub_rn(ur, ul), an.dx[0], hmid, an.dx[1], __fsub_rn(dr, dl), an.dx[2]);
-        f[5][ph] = comb3(__fsub_rn(dl, ul), an.dy[0], vmid, an.dy[1], __fsub_rn(dr, ur), an.dy[2]);
-        f[6][ph] = comb3(__fsub_rn(dr, ul), an.d45[0], vmid, an.d45[1], hmid, an.d45[2]);
-        // (ur-dl)*a0 - vmid*a1 + hmid*a2, evaluated left to right
-        f[7][ph] = __fadd_rn(__fsub_rn(__fmul_rn(__fsub_rn(ur, dl), an.d135[0]), __fmul_rn(vmid, an.d135[1])),
-                             __fmul_rn(hmid, an.d135[2]));
+        f[4][ph] = comb3(sub_rn(ur, ul), an.dx[0], hmid, an.dx[1], sub_rn(dr, dl), an.dx[2]);
+        f[5][ph] = comb3(sub_rn(dl, ul), an.dy[0], vmid, an.dy[1], sub_rn(dr, ur), an.dy[2]);
+        f[6][ph] = comb3(sub_rn(dr, ul), an.d45[0], vmid, an.d45[1], hmid, an.d45[2]);
+        f[7][ph] = d135_unfused(ur, dl, vmid, hmid, an.d135[0], an.d135[1], an.d135[2]);
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
