@@ -568,6 +568,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
     fail(AEISU_ERR_INVALID_ARGUMENT, "Source H/W must be divisible by 4");
   rt.drop_graph();
   rt.configured = false;
+  rt.timed_frames = 0;                 // recorded stage events belong to the previous layout
   rt.batch = batch;
   rt.H = height;
   rt.W = width;
@@ -638,9 +639,8 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
   if (ev) check_hip(hipEventRecord(ev[1], s), "hipEventRecord");
   const float* A = rt.act;
   if (rt.fused) {
-    // one kernel for compress .. expand: the compress and expand stages read zero and the
-    // bottleneck stage times the whole body
-    if (ev) check_hip(hipEventRecord(ev[2], s), "hipEventRecord");
+    // one kernel for compress .. expand, timed as the bottleneck stage (events 1 -> 3;
+    // aeisu_stage_timings reports compress and expand as zero on this path)
     BodyFusedArgs P{};
     P.skip = static_cast<const _Float16*>(rt.skip.ptr);
     P.work = static_cast<_Float16*>(rt.work.ptr);
@@ -656,7 +656,6 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     P.Wl = rt.Wl;
     check_hip(launch_body_fused(m, P, rt.batch, s), "fused body launch");
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
-    if (ev) check_hip(hipEventRecord(ev[4], s), "hipEventRecord");
     return;
   }
   check_hip(launch_compress(m, rt.skip.ptr, rt.compress.frag.ptr, rt.compress.bias.as<float>(),
@@ -706,9 +705,8 @@ static void enqueue_frame(Runtime& rt, const void* d_in, void* d_out, hipStream_
     if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
     return;
   }
-  // fused path: the refine_tail stage is empty, the head stage times the fused kernel
+  // fused path: events 0, 1, 3, 6 only; the head stage times refine + tail + head (3 -> 6)
   enqueue_body(rt, d_in, s, ev);
-  if (ev) check_hip(hipEventRecord(ev[5], s), "hipEventRecord");
   check_hip(launch_fused_tail_head(rt.in_fp32, rt.out_fp32, rt.work.ptr, d_in, rt.refine_tail.frag.ptr,
                                    rt.refine_tail.bias.as<float>(), rt.tail_bias.as<float>(), rt.head.frag.ptr, d_out,
                                    rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.nonfinite.as<unsigned>(),
@@ -954,12 +952,19 @@ int aeisu_stage_timings(aeisu_runtime* h, float ms[AEISU_STAGE_COUNT], int* fram
     Runtime& rt = runtime_of(h);
     if (!ms) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output");
     double acc[AEISU_STAGE_COUNT] = {};
+    // stage s spans events from[s] -> to[s]; on the fused path (one body kernel, one
+    // refine + tail + head kernel) only events 0, 1, 3 and 6 are recorded
+    static const int per_layer_from[6] = {0, 1, 2, 3, 4, 5}, per_layer_to[6] = {1, 2, 3, 4, 5, 6};
+    static const int fused_from[6] = {0, -1, 1, -1, -1, 3}, fused_to[6] = {1, -1, 3, -1, -1, 6};
+    const int* from = rt.fused ? fused_from : per_layer_from;
+    const int* to = rt.fused ? fused_to : per_layer_to;
     for (int f = 0; f < rt.timed_frames; ++f) {
       hipEvent_t* e = &rt.events[size_t(f) * aeisu::kStageEvents];
       aeisu::check_hip(hipEventSynchronize(e[6]), "hipEventSynchronize");
       for (int s = 0; s < 6; ++s) {
+        if (from[s] < 0) continue;
         float t = 0;
-        aeisu::check_hip(hipEventElapsedTime(&t, e[s], e[s + 1]), "hipEventElapsedTime");
+        aeisu::check_hip(hipEventElapsedTime(&t, e[from[s]], e[to[s]]), "hipEventElapsedTime");
         acc[s] += t;
       }
       float total = 0;

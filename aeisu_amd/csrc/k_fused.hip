@@ -312,7 +312,8 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const bool inside = (unsigned)x < (unsigned)G.W;
     chk = fmaf(inside ? u[0] + u[1] + u[2] : 0.f, 0.0f, chk);
     // pair phases (TL, TR) and (BL, BR): after the swap lane groups 0 and 1 both hold
-    // (TL, TR), groups 2 and 3 both hold (BL, BR), and each pair is stored by both groups
+    // (TL, TR), groups 2 and 3 both hold (BL, BR); groups 0 and 2 store each pair (the
+    // duplicates get an out-of-range offset: identical stores would still cost write traffic)
     float left[3], right[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
@@ -323,7 +324,8 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const unsigned o0 = (unsigned)(((size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x) * sizeof(Tout));
 #pragma unroll
     for (int c = 0; c < 3; ++c)
-      fstore_pair<Tout>(ob, inside ? o0 + (unsigned)(c * oplane * sizeof(Tout)) : 0xFFFFFFFFu, left[c], right[c]);
+      fstore_pair<Tout>(ob, inside && (g & 1) == 0 ? o0 + (unsigned)(c * oplane * sizeof(Tout)) : 0xFFFFFFFFu, left[c],
+                        right[c]);
   }
 }
 

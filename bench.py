@@ -7,10 +7,12 @@ head).  Frames are seeded synthetic scenes (aeisu_amd.frames), a pool of
 distinct frames resident in HBM before timing starts.
 
 Protocol:
-  1. W warm-up steps, then K timed steps replaying the per-frame HIP graph,
-     bracketed by torch.cuda.synchronize(): value = K / elapsed (frames/s).
+  1. W warm-up steps, then K timed steps of eager launches (the three kernels of
+     a frame on the current stream), bracketed by torch.cuda.synchronize():
+     value = K / elapsed (frames/s).  The same is measured for replays of the
+     per-frame HIP graph and reported beside it (--graph makes that the value).
   2. K more steps launched eagerly with HIP events recorded on the launch
-     stream around every stage: per-kernel average durations -> roofline.
+     stream around every kernel: per-kernel average durations -> roofline.
   3. CPU baseline: the FP32 oracle restatement of the reference PyTorch path
      (oracle/model.py, tile=0) on a bounded sample of the same frames.
 
@@ -41,6 +43,10 @@ WORKLOADS = {
 }
 
 
+KERNEL_KEYS = {"project_kernel": "project", "body_fused_kernel": "body", "fused_tail_head_kernel": "refine_tail_head",
+               "head_kernel": "head", "refine_tail_kernel": "refine_tail"}
+
+
 def measured_traffic(config: int):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (config 2 only)."""
     path = ROOT / "profiles" / "hbm_traffic_mixed_1080p_pmc.md"
@@ -49,9 +55,7 @@ def measured_traffic(config: int):
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes "):
                 _, name, value = line.split()
-                key = ("refine_tail_head" if name.startswith("fused") else "head" if name.startswith("head")
-                       else "refine_tail" if name.startswith("refine") else name)
-                out[key] = int(value)
+                out[KERNEL_KEYS.get(name, name)] = int(value)
     return out
 
 
@@ -95,7 +99,9 @@ def main():
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--pool", type=int, default=4, help="distinct resident frames cycled through")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline work (0 = skip)")
-    ap.add_argument("--eager", action="store_true", help="time eager launches instead of graph replays")
+    ap.add_argument("--graph", action="store_true",
+                    help="report graph replays as the value (default: eager launches, which are faster here: "
+                         "a graph launch costs more than the three kernel launches it replaces)")
     ap.add_argument("--unfused", action="store_true",
                     help="refine+tail and head as two kernels (coefficients through device memory)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -128,19 +134,24 @@ def main():
         j = i % len(pool)
         model.run(pool[j], out=outs[j], graph=graph, check_finite=False, flags=run_flags)
 
-    # --- 1. timed region: graph replays (or eager) --------------------------------------------------
-    graph = not args.eager
-    for i in range(args.warmup):
-        step(i, graph)
+    # --- 1. timed region: eager launches (three kernels per frame) and graph replays ----------------
+    def timed(graph):
+        for i in range(args.warmup):
+            step(i, graph)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i, graph)
+        torch.cuda.synchronize()
+        return 1000 * (time.perf_counter() - t0) / args.steps
+
     model.run(pool[0], out=outs[0], flags=run_flags)         # finite check once, outside timing
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i, graph)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = 1000 * elapsed / args.steps
-    log(f"bench: {ms_per_step:.4f} ms/step ({'graph' if graph else 'eager'})")
+    graph_ms = timed(True)
+    eager_launch_ms = timed(False)
+    graph = args.graph
+    ms_per_step = graph_ms if graph else eager_launch_ms
+    log(f"bench: {eager_launch_ms:.4f} ms/step eager, {graph_ms:.4f} ms/step graph replay "
+        f"(value from {'graph' if graph else 'eager'})")
 
     # --- 2. per-kernel HIP events on the launch stream ---------------------------------------------
     hd = model.handle(B, H, W, torch.float16, torch.float16, L.FLAG_STAGE_TIMING | run_flags)
@@ -166,14 +177,28 @@ def main():
     refine_bytes = packed_px * (32 * 2 + 64 * 2)              # FP16 refine input + FP16 coefficient output
     refine_flops = 2.0 * packed_px * (32 * 64 * 9 + 64 * 64)
     synth_flops = 2.0 * lr_px * 16 * 100                      # head filter synthesis (MFMA)
-    low_kind = {"fp16": "fp16", "mixed": "fp8", "int8": "int8"}[wl["precision"]]
+    # MFMA the low-precision layers run on: the Mixed policy feeds E4M3 values to the FP16 MFMA
+    # (exact products, FP32 accumulation), INT8 uses the i8 MFMA
+    low_kind = {"fp16": "fp16", "mixed": "fp16", "int8": "int8"}[wl["precision"]]
     ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
     ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
-    ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK["fp16"] + ctrl_flops_low / MFMA_PEAK[low_kind]
-    fused = not args.unfused                                  # refine+tail+head in one kernel
+    fused = not args.unfused                                  # fused body and fused refine+tail+head kernels
     traffic = measured_traffic(args.config)
     kernels = {}
+    proj_bytes = lr_px * 3 * s_io + packed_px * 32 * 2        # RGB in + FP16 skip out
+    ps = stages["project"] / 1000
+    kernels["project"] = {"bound": "hbm", "achieved": proj_bytes / ps / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                          "frac": proj_bytes / ps / HBM_PEAK, "ms": stages["project"],
+                          "algorithmic_bytes": proj_bytes, "traffic": traffic.get("project")}
     if fused:
+        # compress + 4 bottlenecks + expand in one kernel: FP16 skip in, FP16 work out
+        bs_ = stages["bottleneck"] / 1000
+        body_bytes = packed_px * 32 * 2 * 2
+        kernels["body"] = {"bound": "mfma", "achieved": ctrl_flops_low / bs_ / 1e12,
+                           "peak": MFMA_PEAK[low_kind] / 1e12, "unit": "TFLOP/s",
+                           "frac": ctrl_flops_low / bs_ / MFMA_PEAK[low_kind], "ms": stages["bottleneck"],
+                           "algorithmic_flops": ctrl_flops_low, "hbm_gbs": body_bytes / bs_ / 1e9,
+                           "algorithmic_bytes": body_bytes, "traffic": traffic.get("body")}
         # work in + RGB in + 2x RGB out; coefficients never leave the chip
         fused_bytes = packed_px * 32 * 2 + lr_px * (3 * s_io + 12 * s_io)
         fs = stages["head"] / 1000
@@ -183,9 +208,10 @@ def main():
             "traffic": traffic.get("refine_tail_head"),
             "mfma_tflops": (refine_flops + synth_flops) / fs / 1e12,
             "mfma_frac": (refine_flops + synth_flops) / fs / MFMA_PEAK["fp16"]}
-        ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand"))
-        stages.pop("refine_tail")                             # only the event-record gap; no kernel runs there
-        ctrl_ideal_s -= 2.0 * lr_px * (4608 + 1024) / MFMA_PEAK["fp16"]   # refine + tail run inside the fused kernel
+        for k in ("compress", "expand", "refine_tail"):
+            stages.pop(k)                                     # empty on the fused path
+        # controller = project + body + the refine/tail share of the fused kernel (by MFMA count)
+        ctrl_ms = stages["project"] + stages["bottleneck"] + stages["head"] * refine_flops / (refine_flops + synth_flops)
     else:
         head_s = stages["head"] / 1000
         refine_s = stages["refine_tail"] / 1000
@@ -197,6 +223,7 @@ def main():
                                   "frac": refine_flops / refine_s / MFMA_PEAK["fp16"], "ms": stages["refine_tail"],
                                   "algorithmic_flops": refine_flops, "traffic": traffic.get("refine_tail")}
         ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand", "refine_tail"))
+    ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK["fp16"] + ctrl_flops_low / MFMA_PEAK[low_kind]
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     roof = {k: v for k, v in kernels[dominant].items() if k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
     roof["kernel"] = dominant
@@ -226,15 +253,17 @@ def main():
         "data": f"synthetic (aeisu_amd.frames config {args.config}, {args.pool} resident frames)",
         "config": {"workload": wl["name"], "config_id": args.config, "batch": B, "input": [3, H, W],
                    "output": [3, 2 * H, 2 * W], "precision": wl["precision"], "weights": wl["weights"],
-                   "timed": "graph replay" if graph else "eager",
+                   "timed": "graph replay" if graph else "eager launches",
                    "refine_tail_head": "two kernels" if args.unfused else "fused"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,
         "stages_ms": {k: round(v, 5) for k, v in stages.items()},
-        "eager_ms_per_step": round(eager_ms, 5),
+        "eager_ms_per_step": round(eager_launch_ms, 5), "graph_ms_per_step": round(graph_ms, 5),
+        "eager_with_stage_events_ms_per_step": round(eager_ms, 5),
         "controller": {"ms": round(ctrl_ms, 5), "algorithmic_gflop": round((ctrl_flops16 + ctrl_flops_low) / 1e9, 3),
-                       "mfma_frac": ctrl_ideal_s / (ctrl_ms / 1000), "ideal_ms_at_mfma_peak": ctrl_ideal_s * 1000},
+                       "mfma_frac": ctrl_ideal_s / (ctrl_ms / 1000), "ideal_ms_at_mfma_peak": ctrl_ideal_s * 1000,
+                       "low_precision_mfma": low_kind},
         "timing_frames": nframes,
     }
     print(json.dumps(line), flush=True)

@@ -63,11 +63,12 @@ extern "C" {
 
 /* stages reported by aeisu_stage_timings (milliseconds, averaged over recorded frames) */
 #define AEISU_STAGE_PROJECT 0
-#define AEISU_STAGE_COMPRESS 1
-#define AEISU_STAGE_BOTTLENECK 2 /* all four grouped layers */
-#define AEISU_STAGE_EXPAND 3
-#define AEISU_STAGE_REFINE_TAIL 4
-#define AEISU_STAGE_HEAD 5
+#define AEISU_STAGE_COMPRESS 1    /* 0 on the fused path (default) */
+#define AEISU_STAGE_BOTTLENECK 2  /* all four grouped layers; on the fused path the whole body
+                                     kernel (compress, bottlenecks, expand) */
+#define AEISU_STAGE_EXPAND 3      /* 0 on the fused path */
+#define AEISU_STAGE_REFINE_TAIL 4 /* 0 on the fused path */
+#define AEISU_STAGE_HEAD 5        /* reconstruction head; on the fused path refine + tail + head */
 #define AEISU_STAGE_TOTAL 6
 #define AEISU_STAGE_COUNT 7
 
