@@ -16,9 +16,10 @@
 // gfx950 mapping: a block computes an 8x32 packed tile.  The RGB of the tile's
 // 18x66 LR halo region is staged in LDS with coalesced row loads (one global read
 // per source pixel per tile; the next tile's RGB is loaded into registers while the
-// current one is computed), luma of the halo goes to LDS, each thread forms the 32
-// features of one packed pixel into an LDS row, and each wave then runs MFMAs
-// (16x16x32 f16) per 16 pixels against register-resident project weights.
+// current one is computed).  Each thread computes the luma of the 4x4 LR window
+// around its packed pixel and the pixel's 32 features into an LDS row; each wave then
+// runs MFMAs (16x16x32 f16) per 16 of its own pixels against register-resident
+// project weights.  Two workgroup barriers per tile.
 //
 // Two precisions:
 //  * PRECISE = false (Mixed / INT8 policies): features and weights rounded to
@@ -92,7 +93,6 @@ __global__ __launch_bounds__(256) void project_kernel(
     const Tin* __restrict__ src, const h8* __restrict__ wfrag, const float* __restrict__ bias,
     _Float16* __restrict__ skip, Analysis an, int H, int W, int Hq, int Wq, int py, int px, int batch) {
   __shared__ float rgb[3][kPLH][kPLW];
-  __shared__ float luma[kPLH][kPLW + 1];
   __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat<PRECISE>];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -125,12 +125,13 @@ __global__ __launch_bounds__(256) void project_kernel(
       project_fetch<Tin>(st, src, b, 2 * qy0 - 1, 2 * qx0 - 1, H, W, py, px, tid);
     }
   }
+  const int ty = tid / kPTW, tx = tid - ty * kPTW;      // this thread's packed pixel in the tile
   for (int it = 0; it < iters; ++it) {
     const int tidx = tile_of(it, num_tiles);
     if (tidx >= num_tiles) break;
     int b, qy0, qx0;
     origin(tidx, b, qy0, qx0);
-    lds_barrier();                                    // previous tile's LDS reads done
+    lds_barrier();                                    // previous tile's RGB reads done
 #pragma unroll
     for (int i = 0; i < kPStage; ++i) {
       const int q = tid + 256 * i;
@@ -145,14 +146,17 @@ __global__ __launch_bounds__(256) void project_kernel(
       }
     }
     lds_barrier();
-    for (int q = tid; q < kPRgb; q += 256) {
-      const int r = q / kPLW, c = q - r * kPLW;
-      luma[r][c] = dot3_unfused(make_float3(rgb[0][r][c], rgb[1][r][c], rgb[2][r][c]), an.mix[0], an.mix[1],
-                                an.mix[2]);
-    }
-    lds_barrier();
     {
-      const int ty = tid / kPTW, tx = tid - ty * kPTW;
+      // luma of the 4x4 LR window around this packed pixel (halo rows 2ty..2ty+3, columns
+      // 2tx..2tx+3); each 3x3 stencil below reads it around one of the four phase centres
+      float lw[4][4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          lw[a][c] = dot3_unfused(make_float3(rgb[0][2 * ty + a][2 * tx + c], rgb[1][2 * ty + a][2 * tx + c],
+                                              rgb[2][2 * ty + a][2 * tx + c]),
+                                  an.mix[0], an.mix[1], an.mix[2]);
       float f[8][4];
 #pragma unroll
       for (int ph = 0; ph < 4; ++ph) {
@@ -162,9 +166,9 @@ __global__ __launch_bounds__(256) void project_kernel(
         f[0][ph] = dot3_unfused(v, an.basis[0], an.basis[1], an.basis[2]);
         f[1][ph] = dot3_unfused(v, an.basis[3], an.basis[4], an.basis[5]);
         f[2][ph] = dot3_unfused(v, an.basis[6], an.basis[7], an.basis[8]);
-        const float ul = luma[r - 1][c - 1], uc = luma[r - 1][c], ur = luma[r - 1][c + 1];
-        const float cl = luma[r][c - 1], cc = luma[r][c], cr = luma[r][c + 1];
-        const float dl = luma[r + 1][c - 1], dc = luma[r + 1][c], dr = luma[r + 1][c + 1];
+        const float ul = lw[i][j], uc = lw[i][j + 1], ur = lw[i][j + 2];
+        const float cl = lw[i + 1][j], cc = lw[i + 1][j + 1], cr = lw[i + 1][j + 2];
+        const float dl = lw[i + 2][j], dc = lw[i + 2][j + 1], dr = lw[i + 2][j + 2];
         const float hmid = sub_rn(cr, cl), vmid = sub_rn(dc, uc);
         f[3][ph] = cc;
         f[4][ph] = comb3(sub_rn(ur, ul), an.dx[0], hmid, an.dx[1], sub_rn(dr, dl), an.dx[2]);
@@ -185,29 +189,39 @@ __global__ __launch_bounds__(256) void project_kernel(
         if constexpr (PRECISE) *reinterpret_cast<h8*>(&feat[tid][32 + 8 * q]) = r;
       }
     }
-    lds_barrier();
+    // A wave's MFMAs read only the feature rows its own lanes wrote: LDS operations of one wave
+    // execute in order, so a compiler fence (no workgroup barrier) is enough here.
+    asm volatile("" ::: "memory");
+    h8 bop[4], blo[4];
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       const int p = wave * 64 + jg * 16 + n;          // pixel index inside the tile
-      const int ty = p / kPTW, tx = p - ty * kPTW;
-      const h8 bop = *reinterpret_cast<const h8*>(&feat[p][8 * g]);
-      f4 a0 = mfma_f16(A0, bop, f4{0.f, 0.f, 0.f, 0.f});
-      f4 a1 = mfma_f16(A1, bop, f4{0.f, 0.f, 0.f, 0.f});
+      bop[jg] = *reinterpret_cast<const h8*>(&feat[p][8 * g]);
+      if constexpr (PRECISE) blo[jg] = *reinterpret_cast<const h8*>(&feat[p][32 + 8 * g]);
+    }
+    f4 a0[4], a1[4];
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      a0[jg] = mfma_f16(A0, bop[jg], f4{0.f, 0.f, 0.f, 0.f});
+      a1[jg] = mfma_f16(A1, bop[jg], f4{0.f, 0.f, 0.f, 0.f});
       if constexpr (PRECISE) {
-        const h8 blo = *reinterpret_cast<const h8*>(&feat[p][32 + 8 * g]);
-        a0 = mfma_f16(L0, bop, a0);
-        a1 = mfma_f16(L1, bop, a1);
-        a0 = mfma_f16(A0, blo, a0);
-        a1 = mfma_f16(A1, blo, a1);
+        a0[jg] = mfma_f16(L0, bop[jg], a0[jg]);
+        a1[jg] = mfma_f16(L1, bop[jg], a1[jg]);
+        a0[jg] = mfma_f16(A0, blo[jg], a0[jg]);
+        a1[jg] = mfma_f16(A1, blo[jg], a1[jg]);
       }
-      const int qy = qy0 + ty, qx = qx0 + tx;
+    }
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const int p = wave * 64 + jg * 16 + n;
+      const int qy = qy0 + p / kPTW, qx = qx0 + p % kPTW;
       if (qy < Hq && qx < Wq) {
         _Float16* dst = skip + (((size_t)b * Hq + qy) * Wq + qx) * 32 + 4 * g;
         u2 w0, w1;
-        w0[0] = pack_h2(leaky(a0[0] + bs[0][0], 0.1f), leaky(a0[1] + bs[0][1], 0.1f));
-        w0[1] = pack_h2(leaky(a0[2] + bs[0][2], 0.1f), leaky(a0[3] + bs[0][3], 0.1f));
-        w1[0] = pack_h2(leaky(a1[0] + bs[1][0], 0.1f), leaky(a1[1] + bs[1][1], 0.1f));
-        w1[1] = pack_h2(leaky(a1[2] + bs[1][2], 0.1f), leaky(a1[3] + bs[1][3], 0.1f));
+        w0[0] = pack_h2(leaky(a0[jg][0] + bs[0][0], 0.1f), leaky(a0[jg][1] + bs[0][1], 0.1f));
+        w0[1] = pack_h2(leaky(a0[jg][2] + bs[0][2], 0.1f), leaky(a0[jg][3] + bs[0][3], 0.1f));
+        w1[0] = pack_h2(leaky(a1[jg][0] + bs[1][0], 0.1f), leaky(a1[jg][1] + bs[1][1], 0.1f));
+        w1[1] = pack_h2(leaky(a1[jg][2] + bs[1][2], 0.1f), leaky(a1[jg][3] + bs[1][3], 0.1f));
         *reinterpret_cast<u2*>(dst) = w0;
         *reinterpret_cast<u2*>(dst + 16) = w1;
       }
