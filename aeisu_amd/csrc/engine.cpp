@@ -267,6 +267,7 @@ struct Runtime {
   float analysis[24];
   float act[10] = {};
   LayerDev project, compress, grouped[4], expand, refine_tail, head;
+  DeviceBuffer compress_rgb;       // compress weights in the project-output K order (fused body, frame input)
   DeviceBuffer tail_bias;
   DeviceBuffer body_consts;        // epilogue constants of the fused body (kBodyConsts floats)
   // geometry
@@ -279,6 +280,8 @@ struct Runtime {
   int nlow = 2;
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
+  bool fused_rgb = false;          // the fused body takes the frames (project recomputed on chip,
+                                   // no skip tensor); Mixed and INT8 policies
   bool fused_ready = false;        // fused kernels' LDS limit raised on this device
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
   // captured frame graphs, one per (input, output) buffer pair (a small LRU-free cache)
@@ -442,6 +445,17 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
         }));
       else
         dst.frag.upload(pack_frags<uint16_t>(nfrag, 8, [&](int f, int m, int s) { return (uint16_t)fn(f, m, s); }));
+      if (li == 0 && rt.mode == 3) {
+        // frame-input fused body: slot 8g + j of phase chunk kappa takes the project accumulator
+        // channel pc(g, j) = 4g + j (j < 4) or 16 + 4g + j - 4
+        auto pfn = [&](int f, int m, int s) {
+          const int g = s / 8, j = s % 8, c = j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
+          return W(16 * (f / 4) + m, c * 4 + (f % 4), 0);
+        };
+        rt.compress_rgb.upload(pack_frags<uint16_t>(16, 8, [&](int f, int m, int s) {
+          return f32_to_f16_bits(e4m3_value((uint8_t)pfn(f, m, s)));
+        }));
+      }
       if (fp8) {
         const int s_in = li == 0 ? 1 : li + 1;  // compress s1, bottleneck i s(i+2), expand s6
         const TensorView& ws = a.need(l + ".weight_scale", kF32, {cout});
@@ -462,6 +476,13 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
           const int ph = 2 * k + (g >> 1), c = 16 * (g & 1) + i;
           return W(16 * T + m, c * 4 + ph, 0);
         });
+        // frame-input fused body: slots 16g + i take phase 2k + (i >= 8), project accumulator
+        // channel pc(g, i & 7)
+        rt.compress_rgb.upload(pack_frags<int8_t>(8, 16, [&](int f, int m, int s) {
+          const int T = f / 2, k = f % 2, g = s / 16, i = s % 16, j = i & 7;
+          const int ph = 2 * k + (i >> 3), c = j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
+          return W(16 * T + m, c * 4 + ph, 0);
+        }));
       } else if (li == 5) {
         img = pack_frags<int8_t>(8, 16, [&](int T, int m, int s) {
           return W((16 * (T >> 2) + m) * 4 + (T & 3), s, 0);
@@ -498,6 +519,7 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
       cst[640 + j] = staged_f32(rt.expand.bias, o);
       cst[768 + j] = rt.mode ? staged_f32(rt.expand.scale, o) : 0.f;
     }
+    for (int c = 0; c < 32; ++c) cst[896 + c] = staged_f32(rt.project.bias, c);
     rt.body_consts.upload(cst);
   }
 
@@ -545,6 +567,7 @@ static void commit_weights(Runtime& rt) {
     l->bias.commit();
     l->scale.commit();
   }
+  rt.compress_rgb.commit();
   rt.tail_bias.commit();
   rt.body_consts.commit();
 }
@@ -593,13 +616,16 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.out_fp32 = out_layout == AEISU_LAYOUT_NCHW_F32;
   rt.flags = flags;
   const size_t packed = size_t(batch) * rt.Hq * rt.Wq, lowpx = size_t(batch) * rt.Hl * rt.Wl;
-  rt.skip.alloc(packed * 32 * 2);
+  const bool fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
+  // the skip tensor only exists in device memory where the project kernel runs
+  const bool fused_rgb = fused && (rt.mode == 2 || rt.mode == 3);
+  if (fused_rgb) rt.skip.release();
+  else rt.skip.alloc(packed * 32 * 2);
   rt.work.alloc(packed * 32 * 2);
   // the coefficient tensor only exists in device memory on the unfused path
   if (flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED)) rt.meta.alloc(packed * 64 * 2);
   else rt.meta.release();
   // low-resolution activations only reach device memory on the per-layer path
-  const bool fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
   rt.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : (fused ? 0 : 2);
   for (int i = 0; i < 5; ++i) {
     if (i < rt.nlow) rt.low[i].alloc(lowpx * 64 * rt.low_elem());
@@ -616,6 +642,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.refine = clamp_grid(refine_num_tiles(batch, rt.Hq, rt.Wq), refine_blocks_per_cu(), cus);
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
   rt.fused = fused;
+  rt.fused_rgb = fused_rgb;
   rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
@@ -634,6 +661,34 @@ static int low_slot(const Runtime& rt, int li) { return rt.nlow == 5 ? li : (li 
 static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_t* ev) {
   const int m = rt.mode;
   if (ev) check_hip(hipEventRecord(ev[0], s), "hipEventRecord");
+  if (rt.fused_rgb) {
+    // analysis + project + compress .. expand in one kernel from the frames, timed as the
+    // bottleneck stage (events 0 -> 3; project, compress and expand report zero)
+    BodyFusedArgs P{};
+    P.frames = d_in;
+    P.work = static_cast<_Float16*>(rt.work.ptr);
+    P.consts = rt.body_consts.as<float>();
+    const LayerDev* layers[6] = {&rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3], &rt.expand};
+    for (int l = 0; l < 6; ++l) {
+      P.frag[l] = layers[l]->frag.ptr;
+      P.inv_out[l] = inv(rt.act[l + 2]);
+    }
+    P.frag[0] = rt.compress_rgb.ptr;
+    P.pfrag = rt.project.frag.ptr;
+    P.inv_in = inv(rt.act[1]);
+    P.s_out = rt.act[7];
+    for (int i = 0; i < 24; ++i) P.analysis[i] = rt.analysis[i];
+    P.Hl = rt.Hl;
+    P.Wl = rt.Wl;
+    P.H = rt.H;
+    P.W = rt.W;
+    P.py = rt.py;
+    P.px = rt.px;
+    check_hip(launch_body_fused(m, rt.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16, P, rt.batch, s),
+              "fused body launch");
+    if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
+    return;
+  }
   check_hip(launch_project(rt.in_fp32, rt.project_precise, d_in, rt.project.frag.ptr, rt.project.bias.as<float>(), rt.skip.ptr, rt.analysis,
                            rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.grid.project, s), "project launch");
   if (ev) check_hip(hipEventRecord(ev[1], s), "hipEventRecord");
@@ -654,7 +709,7 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     P.s_out = m ? A[7] : 0.f;
     P.Hl = rt.Hl;
     P.Wl = rt.Wl;
-    check_hip(launch_body_fused(m, P, rt.batch, s), "fused body launch");
+    check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, s), "fused body launch");
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }
@@ -705,7 +760,7 @@ static void enqueue_frame(Runtime& rt, const void* d_in, void* d_out, hipStream_
     if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
     return;
   }
-  // fused path: events 0, 1, 3, 6 only; the head stage times refine + tail + head (3 -> 6)
+  // fused path: events 0, (1,) 3, 6 only; the head stage times refine + tail + head (3 -> 6)
   enqueue_body(rt, d_in, s, ev);
   check_hip(launch_fused_tail_head(rt.in_fp32, rt.out_fp32, rt.work.ptr, d_in, rt.refine_tail.frag.ptr,
                                    rt.refine_tail.bias.as<float>(), rt.tail_bias.as<float>(), rt.head.frag.ptr, d_out,
@@ -919,7 +974,12 @@ int aeisu_copy_intermediate(aeisu_runtime* h, int which, void* d_dst, size_t byt
     const size_t need = aeisu_intermediate_bytes(h, which);
     if (need == 0 || bytes != need || !d_dst) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "bad intermediate id, size or pointer");
     const void* src = nullptr;
-    if (which == AEISU_BUF_SKIP) src = rt.skip.ptr;
+    if (which == AEISU_BUF_SKIP) {
+      if (!rt.skip.ptr)
+        aeisu::fail(AEISU_ERR_STATE, "the fused body recomputes the skip tensor on chip for this policy; configure "
+                                     "with AEISU_FLAG_UNFUSED or AEISU_FLAG_KEEP_INTERMEDIATES to read it");
+      src = rt.skip.ptr;
+    }
     else if (which == AEISU_BUF_WORK) src = rt.work.ptr;
     else if (which == AEISU_BUF_META) {
       if (!rt.meta.ptr)
@@ -953,11 +1013,13 @@ int aeisu_stage_timings(aeisu_runtime* h, float ms[AEISU_STAGE_COUNT], int* fram
     if (!ms) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output");
     double acc[AEISU_STAGE_COUNT] = {};
     // stage s spans events from[s] -> to[s]; on the fused path (one body kernel, one
-    // refine + tail + head kernel) only events 0, 1, 3 and 6 are recorded
+    // refine + tail + head kernel) only events 0, 1, 3 and 6 are recorded, and 0, 3, 6 when the
+    // fused body also computes the project from the frames
     static const int per_layer_from[6] = {0, 1, 2, 3, 4, 5}, per_layer_to[6] = {1, 2, 3, 4, 5, 6};
     static const int fused_from[6] = {0, -1, 1, -1, -1, 3}, fused_to[6] = {1, -1, 3, -1, -1, 6};
-    const int* from = rt.fused ? fused_from : per_layer_from;
-    const int* to = rt.fused ? fused_to : per_layer_to;
+    static const int rgb_from[6] = {-1, -1, 0, -1, -1, 3}, rgb_to[6] = {-1, -1, 3, -1, -1, 6};
+    const int* from = rt.fused_rgb ? rgb_from : rt.fused ? fused_from : per_layer_from;
+    const int* to = rt.fused_rgb ? rgb_to : rt.fused ? fused_to : per_layer_to;
     for (int f = 0; f < rt.timed_frames; ++f) {
       hipEvent_t* e = &rt.events[size_t(f) * aeisu::kStageEvents];
       aeisu::check_hip(hipEventSynchronize(e[6]), "hipEventSynchronize");

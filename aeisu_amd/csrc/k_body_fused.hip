@@ -1,15 +1,28 @@
 // Fused low-resolution body: unshuffle + compress 1x1 (128 -> 64), the four grouped 3x3
 // layers (2 groups of 32 -> 32) and expand 1x1 (64 -> 128) + pixel_shuffle + skip add, in one
 // kernel.  The 64-channel activations of a tile never leave the CU: they ping-pong between
-// two LDS buffers, and only the FP16 skip tensor is read and the FP16 work tensor written.
+// two LDS buffers; only the FP16 work tensor is written.
 //
-// Reference: aeisu/model.py:482-489; the Mixed deployment's per-layer kernels
-// SrcPyrNativeFp8Compress.cuh:94-129,222-236, SrcPyrNativeFp8Conv.cuh:414-632,
-// SrcPyrNativeFp8Expand.cuh:68-307 (one launch per layer, activations through device memory);
-// INT8: optimized/shader/src/int8_kernels.cuh:2-62.
+// Reference: aeisu/model.py:473-489 (analysis, project, body); the Mixed deployment's
+// per-layer kernels SrcPyrCudaRuntime.cu:2360-2584 (project), SrcPyrNativeFp8Compress.cuh:
+// 94-129,222-236, SrcPyrNativeFp8Conv.cuh:414-632, SrcPyrNativeFp8Expand.cuh:68-307 (one
+// launch per layer, activations and the skip tensor through device memory); INT8:
+// optimized/shader/src/int8_kernels.cuh:2-62.
 //
-// Arithmetic is that of the per-layer kernels in k_body.hip (same MFMA operands and K order,
-// same epilogues), so the work tensor is bit-identical to compress -> 4 x grouped -> expand.
+// Two inputs:
+//  * BodySrc::Skip: the FP16 skip tensor written by project_kernel (per-layer-compatible path).
+//  * BodySrc::Frames16 / Frames32 (Mixed and INT8 policies): the source frames.  The kernel
+//    recomputes the analysis
+//    features and the project 1x1 for every packed pixel the compress halo needs, feeds the
+//    project accumulators to the compress MFMA as register operands (the compress weights are
+//    packed in the project-output K order), and recomputes the tile centre's skip values for
+//    the expand residual, so the 35 MB (1080p) skip tensor and its halo re-reads never touch
+//    device memory.  Features are those of features.hpp and the project arithmetic that of
+//    project_kernel, so the skip values are bit-identical.
+//
+// Arithmetic is that of the per-layer kernels in k_body.hip (same MFMA operands, same
+// epilogues), so the work tensor is bit-identical to project -> compress -> 4 x grouped ->
+// expand.
 //
 // Tiling: one block per output tile of T x T low pixels.  A 3x3 layer shrinks its input
 // region by one pixel per side, so compress computes the (T+8)^2 region R0, bottleneck i the
@@ -24,12 +37,22 @@
 // all waves; in a grouped layer, wave w serves group w & 1 and keeps that group's 18 weight
 // fragments in registers for the layer.
 //
+// Frame input, per 16-low-pixel group (64 packed pixels, one per lane): the wave stages the
+// group's RGB (6 LR rows x up to 68 columns per channel: one or two row segments when the
+// group wraps a region row) in its own 5 KB LDS slice -- the slices live in the second
+// activation buffer, which is free during compress and expand -- with the next group's RGB in
+// flight in registers.  Each lane computes the 32 features of one packed pixel into the slice
+// (over the RGB: a wave's LDS operations execute in order), the project MFMA reads them back
+// as operands, and its accumulators become the skip operands.  No workgroup barrier is needed
+// inside compress or expand.
+//
 // Latency: the layers hand over through LDS only, so the barrier between layers waits for LDS
 // (lgkmcnt) and not for global loads; each wave issues the next layer's weight fragments
-// before the barrier.  Compress prefetches the skip operands of its next pixel group, expand
-// issues its skip loads before the MFMAs.  Blocks are mapped to tiles in XCD bands, so the
+// before the barrier.  Compress prefetches the operands of its next pixel group, expand
+// issues its global loads before the MFMAs.  Blocks are mapped to tiles in XCD bands, so the
 // tiles whose compress halos overlap run in the same L2.
 #include "common.hpp"
+#include "features.hpp"
 #include "kernels.hpp"
 
 namespace aeisu {
@@ -39,9 +62,10 @@ struct BodyFusedCfg {
   static constexpr int T = MODE == 0 ? 16 : 24;     // output tile side (low pixels)
   static constexpr int PIX = MODE == 0 ? 144 : 72;  // LDS bytes per pixel: 64 channels + pad
   static constexpr int S0 = T + 8;                  // compress region side
+  static constexpr int SizeC = kBodyConsts * 4 + 48;   // constants + 10 group counters (+ pad)
   static constexpr int SizeA = S0 * S0 * PIX;
   static constexpr int SizeB = (S0 - 2) * (S0 - 2) * PIX;
-  static constexpr int Lds = SizeA + SizeB + kBodyConsts * 4;
+  static constexpr int Lds = SizeC + SizeA + SizeB;  // layout: constants | A | B
   static constexpr int Threads = 768, Waves = Threads / 64;
   static_assert(Lds <= 160 * 1024, "fused body LDS exceeds the CU's 160 KB");
   typedef typename std::conditional<MODE == 0 || MODE == 3, h8,
@@ -50,10 +74,13 @@ struct BodyFusedCfg {
   static constexpr int NKc = MODE == 2 ? 2 : 4;     // compress K-chunks
   static constexpr int NKg = MODE == 2 ? 5 : 9;     // grouped K-chunks (taps; i8 packs 2 taps)
   static constexpr int NKe = MODE == 2 ? 1 : 2;     // expand K-chunks
+  // frame input: compress, later expand, weight fragments in LDS after the second buffer
+  static constexpr int FragBytes = (4 * NKc > 8 * NKe ? 4 * NKc : 8 * NKe) * 64 * (int)sizeof(Frag);
+  static constexpr int LdsRgb = Lds + FragBytes;   // used by MODE 2 and 3 only
 };
 
 // LDS constant table (floats), filled from BodyFusedArgs::consts.
-constexpr int kCstCompress = 0, kCstGrouped = 128, kCstExpand = 640;
+constexpr int kCstCompress = 0, kCstGrouped = 128, kCstExpand = 640, kCstProject = 896;
 
 struct BodyTileF {
   int b, y0, x0;
@@ -69,6 +96,15 @@ __device__ __forceinline__ FragSet<MODE, N> load_frags(const void* base, int fir
 #pragma unroll
   for (int i = 0; i < N; ++i) r.f[i] = reinterpret_cast<const typename BodyFusedCfg<MODE>::Frag*>(base)[(first + i) * 64 + lane];
   return r;
+}
+
+// Next group of a phase for this wave: the first Waves groups are dealt statically (wave w
+// takes group w), the rest are claimed from a counter in LDS, so waves that the SIMD issues
+// more often take more groups and all waves leave the phase together.
+__device__ __forceinline__ int claim_group(int* counter, int lane) {
+  int v = 0;
+  if (lane == 0) v = atomicAdd(counter, 1);
+  return __builtin_amdgcn_readfirstlane(v);
 }
 
 // ---- operand and epilogue helpers ---------------------------------------------------------------
@@ -160,28 +196,233 @@ __device__ __forceinline__ void compress_fetch(u4 (&raw)[4], const _Float16* __r
   }
 }
 
+// Compress MFMAs of one 16-pixel group from its skip operands raw[] (FP16 skip values, 8 per
+// u4 in the lane's K-slot order).
+template <int MODE>
+__device__ __forceinline__ void compress_mma(const u4 (&raw)[4], const FragSet<MODE, 4 * BodyFusedCfg<MODE>::NKc>& F,
+                                             float inv_in, typename BodyFusedCfg<MODE>::Acc (&acc)[4]) {
+  typedef BodyFusedCfg<MODE> C;
+  typedef typename C::Frag Frag;
+  constexpr int NK = C::NKc;
+#pragma unroll
+  for (int T = 0; T < 4; ++T) acc[T] = typename C::Acc{};
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    Frag bop;
+    if constexpr (MODE == 2) {
+      const u4 r0 = raw[2 * k], r1 = raw[2 * k + 1];
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        bop[w] = (int)pack_s8x4(quant_s8(h2f_lo(r0[2 * w]), inv_in), quant_s8(h2f_hi(r0[2 * w]), inv_in),
+                                quant_s8(h2f_lo(r0[2 * w + 1]), inv_in), quant_s8(h2f_hi(r0[2 * w + 1]), inv_in));
+        bop[2 + w] = (int)pack_s8x4(quant_s8(h2f_lo(r1[2 * w]), inv_in), quant_s8(h2f_hi(r1[2 * w]), inv_in),
+                                    quant_s8(h2f_lo(r1[2 * w + 1]), inv_in), quant_s8(h2f_hi(r1[2 * w + 1]), inv_in));
+      }
+    } else if constexpr (MODE == 0) {
+      bop = __builtin_bit_cast(h8, raw[k]);
+    } else {
+      const unsigned lo = pack_e4m3x4(h2f_lo_mul(raw[k][0], inv_in), h2f_hi_mul(raw[k][0], inv_in),
+                                      h2f_lo_mul(raw[k][1], inv_in), h2f_hi_mul(raw[k][1], inv_in));
+      const unsigned hi = pack_e4m3x4(h2f_lo_mul(raw[k][2], inv_in), h2f_hi_mul(raw[k][2], inv_in),
+                                      h2f_lo_mul(raw[k][3], inv_in), h2f_hi_mul(raw[k][3], inv_in));
+      if constexpr (MODE == 1) bop = (long)(((unsigned long)hi << 32) | lo);
+      else bop = e4m3x8_to_h8(lo, hi);
+    }
+#pragma unroll
+    for (int T = 0; T < 4; ++T) acc[T] = mma<MODE>(F.f[T * NK + k], bop, acc[T]);
+  }
+}
+
+// Compress epilogue of group pg of region R0 into LDS (zero outside the low grid).
+template <int MODE>
+__device__ __forceinline__ void compress_store(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst, const float* cst,
+                                               const typename BodyFusedCfg<MODE>::Acc (&acc)[4], int pg, int lane) {
+  typedef BodyFusedCfg<MODE> C;
+  constexpr int S = C::S0, N = S * S;
+  const int n = lane & 15, g = lane >> 4;
+  const int q = pg * 16 + n;
+  if (q < N) {
+    const int r = q / S, c = q - r * S;
+    const int gy = t.y0 - 4 + r, gx = t.x0 - 4 + c;
+    const bool inside = ((unsigned)gy < (unsigned)P.Hl) & ((unsigned)gx < (unsigned)P.Wl);   // no branch
+#pragma unroll
+    for (int T = 0; T < 4; ++T) {
+      const int c0 = 16 * T + 4 * g;
+      store_act4<MODE>(dst + q * C::PIX + ch_off<MODE>(c0), acc[T], *reinterpret_cast<const f4*>(cst + kCstCompress + c0),
+                       *reinterpret_cast<const f4*>(cst + kCstCompress + 64 + c0), P.inv_out[0], inside);
+    }
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ void fb_compress(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst, const float* cst,
                                             const FragSet<MODE, 4 * BodyFusedCfg<MODE>::NKc>& F, u4 (&rawN)[4],
                                             int wave, int lane) {
   typedef BodyFusedCfg<MODE> C;
-  typedef typename C::Frag Frag;
-  typedef typename C::Acc Acc;
-  constexpr int S = C::S0, N = S * S, G = (N + 15) / 16, NK = C::NKc;
-  const int n = lane & 15, g = lane >> 4;
+  constexpr int S = C::S0, N = S * S, G = (N + 15) / 16;
   const _Float16* skip = P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32;
-  const float inv_in = P.inv_in, inv_out = P.inv_out[0];
   for (int pg = wave; pg < G; pg += C::Waves) {
     u4 raw[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) raw[k] = rawN[k];
     if (pg + C::Waves < G) compress_fetch<MODE>(rawN, skip, t, pg + C::Waves, P.Hl, P.Wl, lane);
-    Acc acc[4] = {};
+    typename C::Acc acc[4];
+    compress_mma<MODE>(raw, F, P.inv_in, acc);
+    compress_store<MODE>(P, t, dst, cst, acc, pg, lane);
+  }
+}
+
+// ---- frame input: RGB staging, analysis features and project per 16-pixel group -----------------
+// A group of a flattened region (side S >= 16, low-grid origin (oy, ox)) covers at most two row
+// segments: m pixels of region row r from column c, then 16 - m pixels of row r + 1 from column 0.
+// Its RGB stage holds, per channel, the 6 padded-LR rows 4 ly - 1 .. 4 ly + 4 of each segment's
+// low row ly, side by side: segment 1 in stage columns 0 .. 4m + 1, segment 2 after it.
+constexpr int kSW = 68, kSR = 6;                      // stage row width, rows per channel
+constexpr int kSPlane = kSR * kSW;                   // floats per channel
+constexpr int kFRow = 40;                            // halves per feature row (32 + 8 pad)
+constexpr int kSlice = 64 * kFRow * 2;               // bytes of a wave's slice (features >= RGB)
+static_assert(3 * kSPlane * 4 <= kSlice, "RGB stage must fit the slice");
+constexpr int kStageLoads = (3 * kSPlane + 63) / 64; // staged values per lane (19 rows x 64 + rest)
+
+struct GroupGeom {
+  int ly, lx1, lx2, m;                               // segment 1 row / first column, segment 2 first column
+};
+__device__ __forceinline__ GroupGeom group_geom(int oy, int ox, int S, int pg) {
+  const int q0 = 16 * pg, r = q0 / S, c = q0 - r * S;
+  GroupGeom gg;
+  gg.ly = oy + r;
+  gg.lx1 = ox + c;
+  gg.lx2 = ox;
+  gg.m = min(16, S - c);
+  return gg;
+}
+
+// Raw staged values in flight (FP16 frames: two per register).
+template <typename Tin>
+struct RgbStage;
+template <>
+struct RgbStage<float> {
+  float v[kStageLoads];
+  __device__ __forceinline__ void set(int e, float x) { v[e] = x; }
+  __device__ __forceinline__ float get(int e) const { return v[e]; }
+};
+template <>
+struct RgbStage<_Float16> {
+  h2 v[(kStageLoads + 1) / 2];
+  __device__ __forceinline__ void set(int e, _Float16 x) { v[e >> 1][e & 1] = x; }
+  __device__ __forceinline__ float get(int e) const { return (float)v[e >> 1][e & 1]; }
+};
+// Values of stage column j (lanes take j = lane for the first 64 columns of every channel
+// row; columns 64..67 of the 18 channel rows are spread over the remaining loads).  Loads are
+// unconditional with clamped coordinates (replicate padding of aeisu/runtime.py:84), held raw.
+__device__ __forceinline__ int stage_src_x(const GroupGeom& gg, int j, int px, int W) {
+  const int seg2 = j >= 4 * gg.m + 2;
+  const int X = seg2 ? 4 * gg.lx2 - 1 + (j - 4 * gg.m - 2) : 4 * gg.lx1 - 1 + j;
+  return min(max(X - px, 0), W - 1);
+}
+template <typename Tin>
+__device__ __forceinline__ void stage_fetch(RgbStage<Tin>& st, const Tin* __restrict__ frame, const GroupGeom& gg,
+                                            const BodyFusedArgs& P, int lane) {
+  const size_t plane = (size_t)P.H * P.W;
+  {
+    const int j = lane;
+    const int sx = stage_src_x(gg, j, P.px, P.W);
+    const int Y0 = 4 * gg.ly - 1 + (j >= 4 * gg.m + 2 ? 4 : 0) - P.py;
+#pragma unroll
+    for (int row = 0; row < kSR; ++row) {
+      const size_t o = (size_t)min(max(Y0 + row, 0), P.H - 1) * P.W + sx;
+#pragma unroll
+      for (int c = 0; c < 3; ++c) st.set(c * kSR + row, frame[c * plane + o]);
+    }
+  }
+#pragma unroll
+  for (int e = 3 * kSR; e < kStageLoads; ++e) {
+    const int v = min(lane + 64 * (e - 3 * kSR), 3 * kSR * (kSW - 64) - 1);
+    const int rc = v >> 2, j = 64 + (v & 3);
+    const int c = rc / kSR, row = rc - c * kSR;
+    const int sx = stage_src_x(gg, j, P.px, P.W);
+    const int Y = 4 * gg.ly - 1 + (j >= 4 * gg.m + 2 ? 4 : 0) + row - P.py;
+    st.set(e, frame[c * plane + (size_t)min(max(Y, 0), P.H - 1) * P.W + sx]);
+  }
+}
+template <typename Tin>
+__device__ __forceinline__ void stage_store(const RgbStage<Tin>& st, float* stg, int lane) {
+#pragma unroll
+  for (int c = 0; c < 3; ++c)
+#pragma unroll
+    for (int row = 0; row < kSR; ++row) stg[c * kSPlane + row * kSW + lane] = st.get(c * kSR + row);
+#pragma unroll
+  for (int e = 3 * kSR; e < kStageLoads; ++e) {
+    const int v = lane + 64 * (e - 3 * kSR);
+    if (v < 3 * kSR * (kSW - 64)) {
+      const int rc = v >> 2, j = 64 + (v & 3);
+      stg[(rc / kSR) * kSPlane + (rc % kSR) * kSW + j] = st.get(e);
+    }
+  }
+}
+
+// Features of the lane's packed pixel (phase g of low pixel n of the group) from the staged
+// RGB into feature row `lane` of the slice.  The rows overwrite the stage: every lane's stage
+// reads were issued before (a wave's LDS operations execute in order).
+__device__ __forceinline__ void features_to_slice(unsigned char* slice, int m, const Analysis& an, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  float f[8][4];
+  const int col = 4 * n + 2 * (g & 1) + (n >= m ? 2 : 0);
+  packed_features(reinterpret_cast<const float*>(slice) + 2 * (g >> 1) * kSW + col, kSPlane, kSW, an, f);
+  h8 hi[4], lo[4];
+  feature_slices<false>(f, hi, lo);
+  _Float16* feat = reinterpret_cast<_Float16*>(slice);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) *reinterpret_cast<h8*>(feat + lane * kFRow + 8 * q) = hi[q];
+}
+
+// Project 1x1 + LeakyReLU of phase k of the group (FP16 operands as in the Mixed / INT8
+// deployment, project_kernel<., false>): the lane's 8 skip channels 4g..4g+3, 16+4g..16+4g+3
+// of phase k of low pixel n as FP16 pairs -- the project accumulator layout, which is the
+// compress operand order of the frame-input weights and the expand residual layout.
+__device__ __forceinline__ u4 project_phase(const unsigned char* slice, const h8 (&pf)[2], f4 bs0, f4 bs1, int k,
+                                            int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  const h8 b = *reinterpret_cast<const h8*>(reinterpret_cast<const _Float16*>(slice) + (16 * k + n) * kFRow + 8 * g);
+  const f4 a0 = mfma_f16(pf[0], b, f4{0.f, 0.f, 0.f, 0.f});
+  const f4 a1 = mfma_f16(pf[1], b, f4{0.f, 0.f, 0.f, 0.f});
+  u4 sk;
+  sk[0] = pack_h2(leaky(a0[0] + bs0[0], 0.1f), leaky(a0[1] + bs0[1], 0.1f));
+  sk[1] = pack_h2(leaky(a0[2] + bs0[2], 0.1f), leaky(a0[3] + bs0[3], 0.1f));
+  sk[2] = pack_h2(leaky(a1[0] + bs1[0], 0.1f), leaky(a1[1] + bs1[1], 0.1f));
+  sk[3] = pack_h2(leaky(a1[2] + bs1[2], 0.1f), leaky(a1[3] + bs1[3], 0.1f));
+  return sk;
+}
+
+// Frame-input compress (quantized policies).  Per group: stage -> features -> next group's RGB
+// loads issued -> per compress K-chunk, the project MFMAs of its phases and the compress MFMAs.
+template <int MODE, typename Tin>
+__device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst,
+                                                const float* cst, const typename BodyFusedCfg<MODE>::Frag* fr,
+                                                const h8 (&pf)[2], const Analysis& an, RgbStage<Tin>& stN,
+                                                unsigned char* slice, int* counter, int wave, int lane) {
+  typedef BodyFusedCfg<MODE> C;
+  constexpr int S = C::S0, N = S * S, G = (N + 15) / 16, NK = C::NKc;
+  static_assert(MODE == 2 || MODE == 3, "frame input serves the Mixed and INT8 policies");
+  const int g = lane >> 4;
+  const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
+  for (int pg = wave, next; pg < G; pg = next) {
+    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), lane);
+    features_to_slice(slice, group_geom(t.y0 - 4, t.x0 - 4, S, pg).m, an, lane);
+    next = claim_group(counter, lane);
+    if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, S, next), P, lane);
+    const f4 bs0 = *reinterpret_cast<const f4*>(cst + kCstProject + 4 * g);
+    const f4 bs1 = *reinterpret_cast<const f4*>(cst + kCstProject + 16 + 4 * g);
+    typename C::Acc acc[4];
+#pragma unroll
+    for (int T = 0; T < 4; ++T) acc[T] = typename C::Acc{};
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
-      Frag bop;
+      typename C::Frag bop;
       if constexpr (MODE == 2) {
-        const u4 r0 = raw[2 * k], r1 = raw[2 * k + 1];
+        const u4 r0 = project_phase(slice, pf, bs0, bs1, 2 * k, lane);
+        const u4 r1 = project_phase(slice, pf, bs0, bs1, 2 * k + 1, lane);
+        const float inv_in = P.inv_in;
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
           bop[w] = (int)pack_s8x4(quant_s8(h2f_lo(r0[2 * w]), inv_in), quant_s8(h2f_hi(r0[2 * w]), inv_in),
@@ -189,32 +430,19 @@ __device__ __forceinline__ void fb_compress(const BodyFusedArgs& P, BodyTileF t,
           bop[2 + w] = (int)pack_s8x4(quant_s8(h2f_lo(r1[2 * w]), inv_in), quant_s8(h2f_hi(r1[2 * w]), inv_in),
                                       quant_s8(h2f_lo(r1[2 * w + 1]), inv_in), quant_s8(h2f_hi(r1[2 * w + 1]), inv_in));
         }
-      } else if constexpr (MODE == 0) {
-        bop = __builtin_bit_cast(h8, raw[k]);
       } else {
-        const unsigned lo = pack_e4m3x4(h2f_lo_mul(raw[k][0], inv_in), h2f_hi_mul(raw[k][0], inv_in),
-                                        h2f_lo_mul(raw[k][1], inv_in), h2f_hi_mul(raw[k][1], inv_in));
-        const unsigned hi = pack_e4m3x4(h2f_lo_mul(raw[k][2], inv_in), h2f_hi_mul(raw[k][2], inv_in),
-                                        h2f_lo_mul(raw[k][3], inv_in), h2f_hi_mul(raw[k][3], inv_in));
-        if constexpr (MODE == 1) bop = (long)(((unsigned long)hi << 32) | lo);
-        else bop = e4m3x8_to_h8(lo, hi);
+        const u4 r = project_phase(slice, pf, bs0, bs1, k, lane);
+        const float inv_in = P.inv_in;
+        const unsigned lo = pack_e4m3x4(h2f_lo_mul(r[0], inv_in), h2f_hi_mul(r[0], inv_in), h2f_lo_mul(r[1], inv_in),
+                                        h2f_hi_mul(r[1], inv_in));
+        const unsigned hi = pack_e4m3x4(h2f_lo_mul(r[2], inv_in), h2f_hi_mul(r[2], inv_in), h2f_lo_mul(r[3], inv_in),
+                                        h2f_hi_mul(r[3], inv_in));
+        bop = e4m3x8_to_h8(lo, hi);
       }
 #pragma unroll
-      for (int T = 0; T < 4; ++T) acc[T] = mma<MODE>(F.f[T * NK + k], bop, acc[T]);
+      for (int T = 0; T < 4; ++T) acc[T] = mma<MODE>(fr[(T * NK + k) * 64 + lane], bop, acc[T]);
     }
-    const int q = pg * 16 + n;
-    if (q < N) {
-      const int r = q / S, c = q - r * S;
-      const int gy = t.y0 - 4 + r, gx = t.x0 - 4 + c;
-      const bool inside = ((unsigned)gy < (unsigned)P.Hl) & ((unsigned)gx < (unsigned)P.Wl);   // no branch
-#pragma unroll
-      for (int T = 0; T < 4; ++T) {
-        const int c0 = 16 * T + 4 * g;
-        store_act4<MODE>(dst + q * C::PIX + ch_off<MODE>(c0), acc[T],
-                         *reinterpret_cast<const f4*>(cst + kCstCompress + c0),
-                         *reinterpret_cast<const f4*>(cst + kCstCompress + 64 + c0), inv_out, inside);
-      }
-    }
+    compress_store<MODE>(P, t, dst, cst, acc, pg, lane);
   }
 }
 
@@ -222,12 +450,12 @@ __device__ __forceinline__ void fb_compress(const BodyFusedArgs& P, BodyTileF t,
 template <int MODE, int L>
 __device__ __forceinline__ void fb_grouped(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
                                            unsigned char* dst, const float* cst,
-                                           const FragSet<MODE, 2 * BodyFusedCfg<MODE>::NKg>& F, int wave, int lane) {
+                                           const FragSet<MODE, 2 * BodyFusedCfg<MODE>::NKg>& F, int* counter, int wave,
+                                           int lane) {
   typedef BodyFusedCfg<MODE> C;
   typedef typename C::Acc Acc;
   constexpr int Sin = C::S0 - 2 * (L - 1), Sout = Sin - 2, N = Sout * Sout, G = (N + 15) / 16;
   constexpr int NK = C::NKg;
-  constexpr int GW = C::Waves / 2;                     // waves per group
   const int n = lane & 15, g = lane >> 4, grp = wave & 1;
   const float inv_out = P.inv_out[L];
   const float* cb = cst + kCstGrouped + 128 * (L - 1);
@@ -239,7 +467,8 @@ __device__ __forceinline__ void fb_grouped(const BodyFusedArgs& P, BodyTileF t, 
     bs[T] = *reinterpret_cast<const f4*>(cb + 32 * grp + 16 * T + 4 * g);
     sc[T] = *reinterpret_cast<const f4*>(cb + 64 + 32 * grp + 16 * T + 4 * g);
   }
-  for (int pg = wave >> 1; pg < G; pg += GW) {
+  for (int pg = wave >> 1, next; pg < G; pg = next) {
+    next = claim_group(counter, lane);               // this conv group's next pixel group
     // lanes past the region end compute the region's last pixel again and store the same bytes
     const int qc = min(pg * 16 + n, N - 1);
     const int r = qc / Sout, c = qc - r * Sout;
@@ -274,16 +503,73 @@ __device__ __forceinline__ size_t expand_offset(int b, int ly, int lx, int T, in
   return (((size_t)b * Hq + 2 * ly + (ph >> 1)) * Wq + 2 * lx + (ph & 1)) * 32 + c0;
 }
 
+// Expand MFMAs of the group's LDS pixel qc.
+template <int MODE, typename FragAt>
+__device__ __forceinline__ void expand_mma(const unsigned char* src, int qc, FragAt F, int g,
+                                           typename BodyFusedCfg<MODE>::Acc (&acc)[8]) {
+  typedef BodyFusedCfg<MODE> C;
+  constexpr int NK = C::NKe;
+  RawOp<MODE> raw[NK];
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+    raw[k] = *reinterpret_cast<const RawOp<MODE>*>(src + qc * C::PIX + (MODE == 2 ? 16 * g : ch_off<MODE>(32 * k + 8 * g)));
+#pragma unroll
+  for (int T = 0; T < 8; ++T) acc[T] = typename C::Acc{};
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const typename C::Frag bop = widen<MODE>(raw[k]);
+#pragma unroll
+    for (int T = 0; T < 8; ++T) acc[T] = mma<MODE>(F(T * NK + k), bop, acc[T]);
+  }
+}
+
+// work = fp16(dequant(expand output) + skip) for low pixel (ly, lx); sk[T] = the lane's four skip
+// channels of output tile T.
+template <int MODE>
+__device__ __forceinline__ void expand_store(const BodyFusedArgs& P, int b, int ly, int lx, const float* cst,
+                                             const typename BodyFusedCfg<MODE>::Acc (&acc)[8], const u2 (&sk)[8], int g) {
+  const int Hq = 2 * P.Hl, Wq = 2 * P.Wl;
+  const float inv_out = P.inv_out[5], s_out = P.s_out;
+#pragma unroll
+  for (int T = 0; T < 8; ++T) {
+    const f4 bs = *reinterpret_cast<const f4*>(cst + kCstExpand + 16 * T + 4 * g);
+    const f4 sc = *reinterpret_cast<const f4*>(cst + kCstExpand + 128 + 16 * T + 4 * g);
+    const float s[4] = {h2f_lo(sk[T][0]), h2f_hi(sk[T][0]), h2f_lo(sk[T][1]), h2f_hi(sk[T][1])};
+    float v[4];
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) v[r4] = (float)(_Float16)leaky(acc[T][r4] + bs[r4], 0.1f) + s[r4];
+    } else if constexpr (MODE == 1 || MODE == 3) {
+      const unsigned qq = pack_e4m3x4(leaky(fmaf(acc[T][0], sc[0], bs[0]), 0.1f) * inv_out,
+                                      leaky(fmaf(acc[T][1], sc[1], bs[1]), 0.1f) * inv_out,
+                                      leaky(fmaf(acc[T][2], sc[2], bs[2]), 0.1f) * inv_out,
+                                      leaky(fmaf(acc[T][3], sc[3], bs[3]), 0.1f) * inv_out);
+      v[0] = fmaf(e4m3_to_f32<0>(qq), s_out, s[0]);
+      v[1] = fmaf(e4m3_to_f32<1>(qq), s_out, s[1]);
+      v[2] = fmaf(e4m3_to_f32<2>(qq), s_out, s[2]);
+      v[3] = fmaf(e4m3_to_f32<3>(qq), s_out, s[3]);
+    } else {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int qi = quant_s8(leaky(fmaf((float)acc[T][r4], sc[r4], bs[r4]), 0.1f), inv_out);
+        v[r4] = fmaf((float)qi, s_out, s[r4]);
+      }
+    }
+    u2 w;
+    w[0] = pack_h2(v[0], v[1]);
+    w[1] = pack_h2(v[2], v[3]);
+    *reinterpret_cast<u2*>(P.work + expand_offset(b, ly, lx, T, g, Hq, Wq)) = w;
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ void fb_expand(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
                                           const float* cst, const FragSet<MODE, 8 * BodyFusedCfg<MODE>::NKe>& F,
                                           int wave, int lane) {
   typedef BodyFusedCfg<MODE> C;
-  typedef typename C::Acc Acc;
-  constexpr int S = C::T, N = S * S, G = (N + 15) / 16, NK = C::NKe;
+  constexpr int S = C::T, N = S * S, G = (N + 15) / 16;
   const int n = lane & 15, g = lane >> 4;
   const int Hq = 2 * P.Hl, Wq = 2 * P.Wl;
-  const float inv_out = P.inv_out[5], s_out = P.s_out;
   for (int pg = wave; pg < G; pg += C::Waves) {
     const int q = pg * 16 + n, qc = min(q, N - 1);
     const int r = qc / S, c = qc - r * S;
@@ -293,48 +579,42 @@ __device__ __forceinline__ void fb_expand(const BodyFusedArgs& P, BodyTileF t, c
     u2 sk[8];                                          // skip operands first: in flight during the MFMAs
 #pragma unroll
     for (int T = 0; T < 8; ++T) sk[T] = *reinterpret_cast<const u2*>(P.skip + expand_offset(t.b, lyc, lxc, T, g, Hq, Wq));
-    RawOp<MODE> raw[NK];
+    typename C::Acc acc[8];
+    expand_mma<MODE>(src, qc, [&](int i) { return F.f[i]; }, g, acc);
+    if (store) expand_store<MODE>(P, t.b, ly, lx, cst, acc, sk, g);
+  }
+}
+
+template <int MODE, typename Tin>
+__device__ __forceinline__ void fb_expand_rgb(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
+                                              const float* cst, const typename BodyFusedCfg<MODE>::Frag* fr,
+                                              const h8 (&pf)[2], const Analysis& an, RgbStage<Tin>& stN,
+                                              unsigned char* slice, int* counter, int wave, int lane) {
+  typedef BodyFusedCfg<MODE> C;
+  constexpr int S = C::T, N = S * S, G = (N + 15) / 16;
+  static_assert(N % 16 == 0, "expand groups cover whole tiles");
+  const int n = lane & 15, g = lane >> 4;
+  const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
+  for (int pg = wave, next; pg < G; pg = next) {
+    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), lane);
+    features_to_slice(slice, group_geom(t.y0, t.x0, S, pg).m, an, lane);
+    next = claim_group(counter, lane);
+    if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, S, next), P, lane);
+    const int q = pg * 16 + n;
+    const int r = q / S, c = q - r * S;
+    const int ly = t.y0 + r, lx = t.x0 + c;
+    typename C::Acc acc[8];
+    expand_mma<MODE>(src, q, [&](int i) { return fr[i * 64 + lane]; }, g, acc);
+    const f4 bs0 = *reinterpret_cast<const f4*>(cst + kCstProject + 4 * g);
+    const f4 bs1 = *reinterpret_cast<const f4*>(cst + kCstProject + 16 + 4 * g);
+    u2 sk[8];
 #pragma unroll
-    for (int k = 0; k < NK; ++k)
-      raw[k] = *reinterpret_cast<const RawOp<MODE>*>(src + qc * C::PIX + (MODE == 2 ? 16 * g : ch_off<MODE>(32 * k + 8 * g)));
-    Acc acc[8] = {};
-#pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const typename C::Frag bop = widen<MODE>(raw[k]);
-#pragma unroll
-      for (int T = 0; T < 8; ++T) acc[T] = mma<MODE>(F.f[T * NK + k], bop, acc[T]);
+    for (int k = 0; k < 4; ++k) {
+      const u4 r4 = project_phase(slice, pf, bs0, bs1, k, lane);
+      sk[k] = u2{r4[0], r4[1]};                      // output tile k: phase k, channels 4g..4g+3
+      sk[k + 4] = u2{r4[2], r4[3]};                  // output tile k + 4: channels 16 + 4g..
     }
-    if (!store) continue;
-#pragma unroll
-    for (int T = 0; T < 8; ++T) {
-      const f4 bs = *reinterpret_cast<const f4*>(cst + kCstExpand + 16 * T + 4 * g);
-      const f4 sc = *reinterpret_cast<const f4*>(cst + kCstExpand + 128 + 16 * T + 4 * g);
-      const float s[4] = {h2f_lo(sk[T][0]), h2f_hi(sk[T][0]), h2f_lo(sk[T][1]), h2f_hi(sk[T][1])};
-      float v[4];
-      if constexpr (MODE == 0) {
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) v[r4] = (float)(_Float16)leaky(acc[T][r4] + bs[r4], 0.1f) + s[r4];
-      } else if constexpr (MODE == 1 || MODE == 3) {
-        const unsigned qq = pack_e4m3x4(leaky(fmaf(acc[T][0], sc[0], bs[0]), 0.1f) * inv_out,
-                                        leaky(fmaf(acc[T][1], sc[1], bs[1]), 0.1f) * inv_out,
-                                        leaky(fmaf(acc[T][2], sc[2], bs[2]), 0.1f) * inv_out,
-                                        leaky(fmaf(acc[T][3], sc[3], bs[3]), 0.1f) * inv_out);
-        v[0] = fmaf(e4m3_to_f32<0>(qq), s_out, s[0]);
-        v[1] = fmaf(e4m3_to_f32<1>(qq), s_out, s[1]);
-        v[2] = fmaf(e4m3_to_f32<2>(qq), s_out, s[2]);
-        v[3] = fmaf(e4m3_to_f32<3>(qq), s_out, s[3]);
-      } else {
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int qi = quant_s8(leaky(fmaf((float)acc[T][r4], sc[r4], bs[r4]), 0.1f), inv_out);
-          v[r4] = fmaf((float)qi, s_out, s[r4]);
-        }
-      }
-      u2 w;
-      w[0] = pack_h2(v[0], v[1]);
-      w[1] = pack_h2(v[2], v[3]);
-      *reinterpret_cast<u2*>(P.work + expand_offset(t.b, ly, lx, T, g, Hq, Wq)) = w;
-    }
+    if (ly < P.Hl && lx < P.Wl) expand_store<MODE>(P, t.b, ly, lx, cst, acc, sk, g);
   }
 }
 
@@ -348,15 +628,22 @@ __device__ __forceinline__ int body_tile_of(int b, int tiles) {
   return start + (b >> 3);
 }
 
-template <int MODE>
+template <int MODE, int SRC>
 __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel(BodyFusedArgs P) {
   typedef BodyFusedCfg<MODE> C;
+  typedef typename std::conditional<SRC == (int)BodySrc::Frames32, float, _Float16>::type Tin;
+  constexpr bool RGB = SRC != (int)BodySrc::Skip;
+  static_assert(!RGB || MODE == 2 || MODE == 3, "frame input serves the Mixed and INT8 policies");
+  static_assert(!RGB || C::Waves * kSlice <= C::SizeB, "the waves' RGB slices must fit the second buffer");
   constexpr int CPT = (kBodyConsts + C::Threads - 1) / C::Threads;   // constants per thread
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  unsigned char* bufA = smem;
-  unsigned char* bufB = smem + C::SizeA;
-  float* cst = reinterpret_cast<float*>(smem + C::SizeA + C::SizeB);
+  float* cst = reinterpret_cast<float*>(smem);
+  // group counters: frame-input compress, expand; then bottleneck l = 1..4, conv group 0 / 1
+  int* counters = reinterpret_cast<int*>(smem + kBodyConsts * 4);
+  unsigned char* bufA = smem + C::SizeC;
+  unsigned char* bufB = bufA + C::SizeA;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  unsigned char* slice = bufB + wave * kSlice;       // frame input: this wave's RGB / feature slice
   const int tx = (P.Wl + C::T - 1) / C::T, ty = (P.Hl + C::T - 1) / C::T;
   const int tidx = body_tile_of((int)blockIdx.x, (int)gridDim.x);
   BodyTileF t;
@@ -364,39 +651,89 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   const int rem = tidx - t.b * tx * ty;
   t.y0 = (rem / tx) * C::T;
   t.x0 = (rem % tx) * C::T;
-  // constants, compress weights and the first skip operands are in flight together
+  // constants, compress weights and the first group's operands are in flight together
   float cv[CPT];
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int i = tid + j * C::Threads;
     cv[j] = i < kBodyConsts ? P.consts[i] : 0.f;
   }
-  const FragSet<MODE, 4 * C::NKc> Fc = load_frags<MODE, 4 * C::NKc>(P.frag[0], 0, lane);
+  FragSet<MODE, 4 * C::NKc> Fc;
+  if constexpr (!RGB) Fc = load_frags<MODE, 4 * C::NKc>(P.frag[0], 0, lane);
+  // frame input: weight fragments of compress, then expand, in LDS (registers go to the
+  // feature and project work); the block copies them in 16-byte chunks
+  static_assert(!RGB || C::LdsRgb <= 160 * 1024, "frame-input body LDS exceeds the CU's 160 KB");
+  constexpr int FragChunks = C::FragBytes / 16, FCPT = (FragChunks + C::Threads - 1) / C::Threads;
+  u4* fr_lds = reinterpret_cast<u4*>(bufB + C::SizeB);
+  const typename C::Frag* fr = reinterpret_cast<const typename C::Frag*>(fr_lds);
+  u4 fchunk[FCPT];
+  if constexpr (RGB) {
+#pragma unroll
+    for (int j = 0; j < FCPT; ++j) {
+      const int i = min(tid + j * C::Threads, FragChunks - 1);
+      fchunk[j] = reinterpret_cast<const u4*>(P.frag[0])[i];
+    }
+  }
   u4 rawN[4];
-  compress_fetch<MODE>(rawN, P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32, t, wave, P.Hl, P.Wl, lane);
+  h8 pf[2];
+  Analysis an;
+  RgbStage<Tin> stN;
+  const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
+  if constexpr (RGB) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) pf[i] = reinterpret_cast<const h8*>(P.pfrag)[i * 64 + lane];
+    an = analysis_from(P.analysis);
+    stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, C::S0, wave), P, lane);
+  } else {
+    compress_fetch<MODE>(rawN, P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32, t, wave, P.Hl, P.Wl, lane);
+  }
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
     const int i = tid + j * C::Threads;
     if (i < kBodyConsts) cst[i] = cv[j];
   }
+  if constexpr (RGB) {
+#pragma unroll
+    for (int j = 0; j < FCPT; ++j)
+      if (tid + j * C::Threads < FragChunks) fr_lds[tid + j * C::Threads] = fchunk[j];
+  }
+  if (tid < 10) counters[tid] = tid < 2 ? C::Waves : C::Waves / 2;
   lds_barrier();
-  fb_compress<MODE>(P, t, bufA, cst, Fc, rawN, wave, lane);
+  if constexpr (RGB) fb_compress_rgb<MODE, Tin>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
+  else fb_compress<MODE>(P, t, bufA, cst, Fc, rawN, wave, lane);
+  if constexpr (RGB) {                                 // expand weights: in flight during the barrier
+#pragma unroll
+    for (int j = 0; j < FCPT; ++j) {
+      const int i = min(tid + j * C::Threads, FragChunks - 1);
+      fchunk[j] = reinterpret_cast<const u4*>(P.frag[5])[i];
+    }
+  }
   const int gf = (wave & 1) * 2 * C::NKg;              // this wave's group's first fragment
   const FragSet<MODE, 2 * C::NKg> F1 = load_frags<MODE, 2 * C::NKg>(P.frag[1], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 1>(P, t, bufA, bufB, cst, F1, wave, lane);
+  if constexpr (RGB) {                                 // compress no longer reads the region
+#pragma unroll
+    for (int j = 0; j < FCPT; ++j)
+      if (tid + j * C::Threads < FragChunks) fr_lds[tid + j * C::Threads] = fchunk[j];
+  }
+  fb_grouped<MODE, 1>(P, t, bufA, bufB, cst, F1, counters + 2 + (wave & 1), wave, lane);
   const FragSet<MODE, 2 * C::NKg> F2 = load_frags<MODE, 2 * C::NKg>(P.frag[2], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 2>(P, t, bufB, bufA, cst, F2, wave, lane);
+  fb_grouped<MODE, 2>(P, t, bufB, bufA, cst, F2, counters + 4 + (wave & 1), wave, lane);
   const FragSet<MODE, 2 * C::NKg> F3 = load_frags<MODE, 2 * C::NKg>(P.frag[3], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 3>(P, t, bufA, bufB, cst, F3, wave, lane);
+  fb_grouped<MODE, 3>(P, t, bufA, bufB, cst, F3, counters + 6 + (wave & 1), wave, lane);
   const FragSet<MODE, 2 * C::NKg> F4 = load_frags<MODE, 2 * C::NKg>(P.frag[4], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 4>(P, t, bufB, bufA, cst, F4, wave, lane);
-  const FragSet<MODE, 8 * C::NKe> Fe = load_frags<MODE, 8 * C::NKe>(P.frag[5], 0, lane);
+  fb_grouped<MODE, 4>(P, t, bufB, bufA, cst, F4, counters + 8 + (wave & 1), wave, lane);
+  // frame input: the first expand group's RGB loads are issued with the expand weights (its
+  // slice in the second buffer is written only after the barrier that ends the bottleneck)
+  if constexpr (RGB) stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, C::T, wave), P, lane);
+  FragSet<MODE, 8 * C::NKe> Fe;
+  if constexpr (!RGB) Fe = load_frags<MODE, 8 * C::NKe>(P.frag[5], 0, lane);
   lds_barrier();
-  fb_expand<MODE>(P, t, bufA, cst, Fe, wave, lane);
+  if constexpr (RGB) fb_expand_rgb<MODE, Tin>(P, t, bufA, cst, fr, pf, an, stN, slice, counters + 1, wave, lane);
+  else fb_expand<MODE>(P, t, bufA, cst, Fe, wave, lane);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -405,31 +742,55 @@ int body_fused_num_tiles(int mode, int batch, int Hl, int Wl) {
   return batch * ((Hl + T - 1) / T) * ((Wl + T - 1) / T);
 }
 
+template <int MODE, int SRC>
+static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&body_fused_kernel<MODE, SRC>); }
+
 hipError_t body_fused_prepare() {
-  const void* k[4] = {reinterpret_cast<const void*>(&body_fused_kernel<0>),
-                      reinterpret_cast<const void*>(&body_fused_kernel<1>),
-                      reinterpret_cast<const void*>(&body_fused_kernel<2>),
-                      reinterpret_cast<const void*>(&body_fused_kernel<3>)};
+  const void* k[4][3] = {{body_kernel_ptr<0, 0>(), nullptr, nullptr},
+                         {body_kernel_ptr<1, 0>(), nullptr, nullptr},
+                         {body_kernel_ptr<2, 0>(), body_kernel_ptr<2, 1>(), body_kernel_ptr<2, 2>()},
+                         {body_kernel_ptr<3, 0>(), body_kernel_ptr<3, 1>(), body_kernel_ptr<3, 2>()}};
   const int lds[4] = {BodyFusedCfg<0>::Lds, BodyFusedCfg<1>::Lds, BodyFusedCfg<2>::Lds, BodyFusedCfg<3>::Lds};
-  for (int i = 0; i < 4; ++i) {
-    const hipError_t e = hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize, lds[i]);
-    if (e != hipSuccess) return e;
-  }
+  const int lds_rgb[4] = {0, 0, BodyFusedCfg<2>::LdsRgb, BodyFusedCfg<3>::LdsRgb};
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 3; ++j) {
+      if (!k[i][j]) continue;
+      const hipError_t e =
+          hipFuncSetAttribute(k[i][j], hipFuncAttributeMaxDynamicSharedMemorySize, j ? lds_rgb[i] : lds[i]);
+      if (e != hipSuccess) return e;
+    }
   return hipSuccess;
 }
 
-hipError_t launch_body_fused(int mode, const BodyFusedArgs& args, int batch, hipStream_t stream) {
-  const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl);
-#define AEISU_BODY(M)                                                                                            \
-  hipLaunchKernelGGL(body_fused_kernel<M>, dim3(tiles), dim3(BodyFusedCfg<M>::Threads), BodyFusedCfg<M>::Lds, \
-                     stream, args)
-  switch (mode) {
-    case 0: AEISU_BODY(0); break;
-    case 1: AEISU_BODY(1); break;
-    case 2: AEISU_BODY(2); break;
-    default: AEISU_BODY(3); break;
+template <int MODE, int SRC>
+static void launch_body_t(const BodyFusedArgs& args, int tiles, hipStream_t stream) {
+  hipLaunchKernelGGL((body_fused_kernel<MODE, SRC>), dim3(tiles), dim3(BodyFusedCfg<MODE>::Threads),
+                     SRC ? BodyFusedCfg<MODE>::LdsRgb : BodyFusedCfg<MODE>::Lds, stream, args);
+}
+template <int MODE>
+static void launch_body_m(BodySrc src, const BodyFusedArgs& args, int tiles, hipStream_t stream) {
+  switch (src) {
+    case BodySrc::Skip: launch_body_t<MODE, 0>(args, tiles, stream); break;
+    case BodySrc::Frames16: launch_body_t<MODE, 1>(args, tiles, stream); break;
+    default: launch_body_t<MODE, 2>(args, tiles, stream); break;
   }
-#undef AEISU_BODY
+}
+
+hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, hipStream_t stream) {
+  const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl);
+  switch (mode) {
+    case 0:
+    case 1:
+      // FP16 policy (FP16 hi/lo project operands) and FP8-MFMA variant (the FP8 MFMA's sum
+      // depends on the K order, so the permuted compress weights would not reproduce the
+      // per-layer result bit for bit): skip input only
+      if (src != BodySrc::Skip) return hipErrorInvalidValue;
+      if (mode == 0) launch_body_t<0, 0>(args, tiles, stream);
+      else launch_body_t<1, 0>(args, tiles, stream);
+      break;
+    case 2: launch_body_m<2>(src, args, tiles, stream); break;
+    default: launch_body_m<3>(src, args, tiles, stream); break;
+  }
   return hipGetLastError();
 }
 

@@ -4,10 +4,9 @@
 // Reference: aeisu/model.py:273-341 (_rgb_to_feature8), 481 (unshuffle,
 // project_540, LeakyReLU); native FusedPackRgbYLearnedRgb4DirAndProjectKernel,
 // optimized/native/src/neural/srcpyr/SrcPyrCudaRuntime.cu:2208-2219, 2360-2584.
-// Learned RGB and luma use explicitly unfused multiplies and adds in the
-// reference's evaluation order, and the directional stencils are evaluated
-// without contraction too, so the FP16-rounded features equal those of the
-// FP32 PyTorch model evaluated on the same input.
+// The features (features.hpp) equal those of the FP32 PyTorch model evaluated
+// on the same input.  This kernel runs on the per-layer path and for FP32 frames;
+// the fused body recomputes the same skip values from RGB instead of reading them.
 //
 // Geometry: packed pixel (qy, qx) covers padded LR pixels (2qy+i, 2qx+j),
 // phase 2i+j, channel = feature*4 + phase; padded LR (Y, X) reads source
@@ -29,36 +28,14 @@
 //    Features and weights are split into FP16 hi + lo parts and the product
 //    is formed as W_hi f_hi + W_lo f_hi + W_hi f_lo (6 MFMAs, FP32 accumulate),
 //    accurate to ~2^-22 relative.
-#include "common.hpp"
+#include "features.hpp"
 
 namespace aeisu {
-
-struct Analysis {
-  float basis[9], mix[3], dx[3], dy[3], d45[3], d135[3];
-};
 
 constexpr int kPTW = 32, kPTH = 8;
 constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
 // halves per LDS feature row: 32 features (+ 32 low parts in the FP32-accurate variant) + 8 pad
 template <bool PRECISE> constexpr int kPFeat = PRECISE ? 72 : 40;
-
-__device__ __forceinline__ float sub_rn(float a, float b) { return a - b; }
-// HIP's __fmul_rn / __fadd_rn are plain operators that the compiler may contract into FMAs
-// (-ffp-contract=fast is the default): contraction is switched off here explicitly.
-__device__ __forceinline__ float dot3_unfused(float3 v, float a, float b, float c) {
-#pragma clang fp contract(off)
-  return (v.x * a + v.y * b) + v.z * c;
-}
-// (p*a + q*b) + r*c, unfused, reference order
-__device__ __forceinline__ float comb3(float p, float a, float q, float b, float r, float c) {
-#pragma clang fp contract(off)
-  return (p * a + q * b) + r * c;
-}
-// (u - d) * a0 - m * a1 + h * a2, evaluated left to right, unfused
-__device__ __forceinline__ float d135_unfused(float u, float d, float m, float h, float a0, float a1, float a2) {
-#pragma clang fp contract(off)
-  return ((u - d) * a0 - m * a1) + h * a2;
-}
 
 constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
 constexpr int kPStage = (3 * kPRgb + 255) / 256;         // staged RGB values per thread
@@ -147,46 +124,14 @@ __global__ __launch_bounds__(256) void project_kernel(
     }
     lds_barrier();
     {
-      // luma of the 4x4 LR window around this packed pixel (halo rows 2ty..2ty+3, columns
-      // 2tx..2tx+3); each 3x3 stencil below reads it around one of the four phase centres
-      float lw[4][4];
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          lw[a][c] = dot3_unfused(make_float3(rgb[0][2 * ty + a][2 * tx + c], rgb[1][2 * ty + a][2 * tx + c],
-                                              rgb[2][2 * ty + a][2 * tx + c]),
-                                  an.mix[0], an.mix[1], an.mix[2]);
       float f[8][4];
-#pragma unroll
-      for (int ph = 0; ph < 4; ++ph) {
-        const int i = ph >> 1, j = ph & 1;
-        const int r = 2 * ty + i + 1, c = 2 * tx + j + 1;   // centre in the halo region
-        const float3 v = make_float3(rgb[0][r][c], rgb[1][r][c], rgb[2][r][c]);
-        f[0][ph] = dot3_unfused(v, an.basis[0], an.basis[1], an.basis[2]);
-        f[1][ph] = dot3_unfused(v, an.basis[3], an.basis[4], an.basis[5]);
-        f[2][ph] = dot3_unfused(v, an.basis[6], an.basis[7], an.basis[8]);
-        const float ul = lw[i][j], uc = lw[i][j + 1], ur = lw[i][j + 2];
-        const float cl = lw[i + 1][j], cc = lw[i + 1][j + 1], cr = lw[i + 1][j + 2];
-        const float dl = lw[i + 2][j], dc = lw[i + 2][j + 1], dr = lw[i + 2][j + 2];
-        const float hmid = sub_rn(cr, cl), vmid = sub_rn(dc, uc);
-        f[3][ph] = cc;
-        f[4][ph] = comb3(sub_rn(ur, ul), an.dx[0], hmid, an.dx[1], sub_rn(dr, dl), an.dx[2]);
-        f[5][ph] = comb3(sub_rn(dl, ul), an.dy[0], vmid, an.dy[1], sub_rn(dr, ur), an.dy[2]);
-        f[6][ph] = comb3(sub_rn(dr, ul), an.d45[0], vmid, an.d45[1], hmid, an.d45[2]);
-        f[7][ph] = d135_unfused(ur, dl, vmid, hmid, an.d135[0], an.d135[1], an.d135[2]);
-      }
+      packed_features(&rgb[0][2 * ty][2 * tx], kPLH * kPLW, kPLW, an, f);
+      h8 hi[4], lo[4];
+      feature_slices<PRECISE>(f, hi, lo);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        h8 v, r;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = f[2 * q + (e >> 2)][e & 3];
-          v[e] = (_Float16)x;
-          r[e] = (_Float16)(x - (float)v[e]);
-        }
-        *reinterpret_cast<h8*>(&feat[tid][8 * q]) = v;
-        if constexpr (PRECISE) *reinterpret_cast<h8*>(&feat[tid][32 + 8 * q]) = r;
+        *reinterpret_cast<h8*>(&feat[tid][8 * q]) = hi[q];
+        if constexpr (PRECISE) *reinterpret_cast<h8*>(&feat[tid][32 + 8 * q]) = lo[q];
       }
     }
     // A wave's MFMAs read only the feature rows its own lanes wrote: LDS operations of one wave
@@ -243,13 +188,7 @@ static void launch_project_t(const void* src, const void* wfrag, const float* bi
 hipError_t launch_project(int in_fp32, int precise, const void* src, const void* wfrag, const float* bias, void* skip,
                           const float* analysis24, int H, int W, int Hq, int Wq, int py, int px, int batch,
                           int grid, hipStream_t stream) {
-  Analysis an;
-  const float* a = analysis24;
-  for (int i = 0; i < 9; ++i) an.basis[i] = a[i];
-  for (int i = 0; i < 3; ++i) {
-    an.mix[i] = a[9 + i]; an.dx[i] = a[12 + i]; an.dy[i] = a[15 + i];
-    an.d45[i] = a[18 + i]; an.d135[i] = a[21 + i];
-  }
+  const Analysis an = analysis_from(analysis24);
   if (in_fp32 && precise) launch_project_t<float, true>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);
   else if (in_fp32) launch_project_t<float, false>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);
   else if (precise) launch_project_t<_Float16, true>(src, wfrag, bias, skip, an, H, W, Hq, Wq, py, px, batch, grid, stream);

@@ -28,25 +28,35 @@ hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* m
 
 // Fused body: compress, the four grouped layers and expand in one kernel (activations in LDS).
 // Layer order in the arrays: 0 compress, 1..4 bottleneck 0..3, 5 expand.
-// consts: the per-channel epilogue constants of all six layers, kBodyConsts floats:
+// consts: the per-channel epilogue constants, kBodyConsts floats:
 //   [0, 64) compress bias, [64, 128) compress scale, then per bottleneck l = 0..3
 //   [128 + 128 l, +64) bias and [+64, +128) scale, then expand [640, 768) bias and
-//   [768, 896) scale, both indexed T * 16 + m for output channel (16 * (T >> 2) + m) * 4 + (T & 3).
-//   Scales are 0 for the FP16 policy.
-constexpr int kBodyConsts = 896;
+//   [768, 896) scale, both indexed T * 16 + m for output channel (16 * (T >> 2) + m) * 4 + (T & 3),
+//   then the project bias [896, 928).  Scales are 0 for the FP16 policy.
+// Input: the skip tensor (BodySrc::Skip, written by the project kernel), or (Mixed and INT8
+// policies) the frames themselves (FP16 / FP32), from which the kernel recomputes analysis features and project
+// for the compress halo and again for the expand residual, so no skip tensor exists.  The
+// frame-input variants take the compress weights in the project-output K order
+// (engine.cpp pack of compress_rgb).
+constexpr int kBodyConsts = 928;
+enum class BodySrc : int { Skip = 0, Frames16 = 1, Frames32 = 2 };
 struct BodyFusedArgs {
-  const _Float16* skip;
+  const _Float16* skip;    // BodySrc::Skip
+  const void* frames;      // frame-input variants: planar [batch][3][H][W]
   _Float16* work;
   const void* frag[6];
+  const void* pfrag;       // project weight fragments (frame-input variants)
   const float* consts;
   float inv_out[6];        // 1 / output activation scale of each layer (quantized policies)
   float inv_in;            // 1 / compress input scale
   float s_out;             // expand output scale (dequantization before the skip add)
+  float analysis[24];      // analysis constants (frame-input variants)
   int Hl, Wl;
+  int H, W, py, px;        // frame geometry (frame-input variants)
 };
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl);
 hipError_t body_fused_prepare();
-hipError_t launch_body_fused(int mode, const BodyFusedArgs& args, int batch, hipStream_t stream);
+hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, hipStream_t stream);
 
 // Fused refine + tail + head (coefficients in LDS); one block per CU (1024 threads for FP16
 // frames, 768 for FP32 frames).

@@ -7,8 +7,8 @@ head).  Frames are seeded synthetic scenes (aeisu_amd.frames), a pool of
 distinct frames resident in HBM before timing starts.
 
 Protocol:
-  1. W warm-up steps, then K timed steps of eager launches (the three kernels of
-     a frame on the current stream), bracketed by torch.cuda.synchronize():
+  1. W warm-up steps, then K timed steps of eager launches (the kernels of a
+     frame on the current stream: two for the quantized policies, three for FP16), bracketed by torch.cuda.synchronize():
      value = K / elapsed (frames/s).  The same is measured for replays of the
      per-frame HIP graph and reported beside it (--graph makes that the value).
   2. K more steps launched eagerly with HIP events recorded on the launch
@@ -134,7 +134,7 @@ def main():
         j = i % len(pool)
         model.run(pool[j], out=outs[j], graph=graph, check_finite=False, flags=run_flags)
 
-    # --- 1. timed region: eager launches (three kernels per frame) and graph replays ----------------
+    # --- 1. timed region: eager launches (the frame's kernels) and graph replays ----------------
     def timed(graph):
         for i in range(args.warmup):
             step(i, graph)
@@ -186,19 +186,28 @@ def main():
     traffic = measured_traffic(args.config)
     kernels = {}
     proj_bytes = lr_px * 3 * s_io + packed_px * 32 * 2        # RGB in + FP16 skip out
-    ps = stages["project"] / 1000
-    kernels["project"] = {"bound": "hbm", "achieved": proj_bytes / ps / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                          "frac": proj_bytes / ps / HBM_PEAK, "ms": stages["project"],
-                          "algorithmic_bytes": proj_bytes, "traffic": traffic.get("project")}
+    proj_flops = 2.0 * packed_px * 32 * 32                    # project 1x1, FP16 MFMA
+    # the quantized policies' fused body computes analysis + project from the frames itself
+    body_has_project = fused and stages["project"] == 0.0
+    if not body_has_project:
+        ps = stages["project"] / 1000
+        kernels["project"] = {"bound": "hbm", "achieved": proj_bytes / ps / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                              "frac": proj_bytes / ps / HBM_PEAK, "ms": stages["project"],
+                              "algorithmic_bytes": proj_bytes, "traffic": traffic.get("project")}
     if fused:
-        # compress + 4 bottlenecks + expand in one kernel: FP16 skip in, FP16 work out
+        # [project +] compress + 4 bottlenecks + expand in one kernel; in: RGB frames (or the FP16
+        # skip tensor), out: FP16 work.  MFMA peak = the flop-weighted peak of the MFMAs it runs.
         bs_ = stages["bottleneck"] / 1000
-        body_bytes = packed_px * 32 * 2 * 2
-        kernels["body"] = {"bound": "mfma", "achieved": ctrl_flops_low / bs_ / 1e12,
-                           "peak": MFMA_PEAK[low_kind] / 1e12, "unit": "TFLOP/s",
-                           "frac": ctrl_flops_low / bs_ / MFMA_PEAK[low_kind], "ms": stages["bottleneck"],
-                           "algorithmic_flops": ctrl_flops_low, "hbm_gbs": body_bytes / bs_ / 1e9,
-                           "algorithmic_bytes": body_bytes, "traffic": traffic.get("body")}
+        bflops = ctrl_flops_low + (proj_flops if body_has_project else 0.0)
+        ideal_s = ctrl_flops_low / MFMA_PEAK[low_kind] + (proj_flops / MFMA_PEAK["fp16"] if body_has_project else 0.0)
+        peak_eff = bflops / ideal_s
+        body_bytes = (lr_px * 3 * s_io + packed_px * 32 * 2) if body_has_project else packed_px * 32 * 2 * 2
+        kernels["body"] = {"bound": "mfma", "achieved": bflops / bs_ / 1e12,
+                           "peak": peak_eff / 1e12, "unit": "TFLOP/s",
+                           "frac": ideal_s / bs_, "ms": stages["bottleneck"],
+                           "algorithmic_flops": bflops, "hbm_gbs": body_bytes / bs_ / 1e9,
+                           "algorithmic_bytes": body_bytes, "traffic": traffic.get("body"),
+                           "includes_project": body_has_project}
         # work in + RGB in + 2x RGB out; coefficients never leave the chip
         fused_bytes = packed_px * 32 * 2 + lr_px * (3 * s_io + 12 * s_io)
         fs = stages["head"] / 1000
@@ -208,10 +217,11 @@ def main():
             "traffic": traffic.get("refine_tail_head"),
             "mfma_tflops": (refine_flops + synth_flops) / fs / 1e12,
             "mfma_frac": (refine_flops + synth_flops) / fs / MFMA_PEAK["fp16"]}
-        for k in ("compress", "expand", "refine_tail"):
+        for k in ("compress", "expand", "refine_tail") + (("project",) if body_has_project else ()):
             stages.pop(k)                                     # empty on the fused path
         # controller = project + body + the refine/tail share of the fused kernel (by MFMA count)
-        ctrl_ms = stages["project"] + stages["bottleneck"] + stages["head"] * refine_flops / (refine_flops + synth_flops)
+        ctrl_ms = (stages.get("project", 0.0) + stages["bottleneck"]
+                   + stages["head"] * refine_flops / (refine_flops + synth_flops))
     else:
         head_s = stages["head"] / 1000
         refine_s = stages["refine_tail"] / 1000
