@@ -47,24 +47,20 @@ __device__ __forceinline__ float d135_unfused(float u, float d, float m, float h
   return ((u - d) * a0 - m * a1) + h * a2;
 }
 
-// Features f[feature][phase] of the packed pixel whose 4x4 LR window (one halo pixel on each
-// side of its 2x2 LR pixels) starts at `w`: channel c of window pixel (a, b) is
-// w[c * plane + a * rs + b].  The luma of the 16 window pixels feeds the 3x3 stencils
-// centred on each of the four LR pixels.
-__device__ __forceinline__ void packed_features(const float* w, int plane, int rs, const Analysis& an,
-                                                float (&f)[8][4]) {
+// Features f[feature][phase] of a packed pixel from its 4x4 LR window w[channel][row][col]
+// (one halo pixel on each side of its 2x2 LR pixels).  The luma of the 16 window pixels feeds
+// the 3x3 stencils centred on each of the four LR pixels.
+__device__ __forceinline__ void window_features(const float (&w)[3][4][4], const Analysis& an, float (&f)[8][4]) {
   float lw[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b)
-      lw[a][b] = dot3_unfused(make_float3(w[a * rs + b], w[plane + a * rs + b], w[2 * plane + a * rs + b]),
-                              an.mix[0], an.mix[1], an.mix[2]);
+      lw[a][b] = dot3_unfused(make_float3(w[0][a][b], w[1][a][b], w[2][a][b]), an.mix[0], an.mix[1], an.mix[2]);
 #pragma unroll
   for (int ph = 0; ph < 4; ++ph) {
     const int i = ph >> 1, j = ph & 1;
-    const int o = (i + 1) * rs + j + 1;                // the LR pixel of this phase
-    const float3 v = make_float3(w[o], w[plane + o], w[2 * plane + o]);
+    const float3 v = make_float3(w[0][i + 1][j + 1], w[1][i + 1][j + 1], w[2][i + 1][j + 1]);   // this phase's pixel
     f[0][ph] = dot3_unfused(v, an.basis[0], an.basis[1], an.basis[2]);
     f[1][ph] = dot3_unfused(v, an.basis[3], an.basis[4], an.basis[5]);
     f[2][ph] = dot3_unfused(v, an.basis[6], an.basis[7], an.basis[8]);
@@ -78,6 +74,19 @@ __device__ __forceinline__ void packed_features(const float* w, int plane, int r
     f[6][ph] = comb3(sub_rn(dr, ul), an.d45[0], vmid, an.d45[1], hmid, an.d45[2]);
     f[7][ph] = d135_unfused(ur, dl, vmid, hmid, an.d135[0], an.d135[1], an.d135[2]);
   }
+}
+
+// The same from LDS: channel c of window pixel (a, b) is p[c * plane + a * rs + b].
+__device__ __forceinline__ void packed_features(const float* p, int plane, int rs, const Analysis& an,
+                                                float (&f)[8][4]) {
+  float w[3][4][4];
+#pragma unroll
+  for (int c = 0; c < 3; ++c)
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w[c][a][b] = p[c * plane + a * rs + b];
+  window_features(w, an, f);
 }
 
 // The 32 features as four MFMA operand slices (slice q = features 2q, 2q+1 at the four

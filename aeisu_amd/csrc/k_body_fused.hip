@@ -366,9 +366,22 @@ __device__ __forceinline__ void stage_store(const RgbStage<Tin>& st, float* stg,
 // reads were issued before (a wave's LDS operations execute in order).
 __device__ __forceinline__ void features_to_slice(unsigned char* slice, int m, const Analysis& an, int lane) {
   const int n = lane & 15, g = lane >> 4;
-  float f[8][4];
+  // window origin: an even stage column, so each window row is two aligned float2 reads; all
+  // 24 reads are issued before the arithmetic
   const int col = 4 * n + 2 * (g & 1) + (n >= m ? 2 : 0);
-  packed_features(reinterpret_cast<const float*>(slice) + 2 * (g >> 1) * kSW + col, kSPlane, kSW, an, f);
+  const float* p = reinterpret_cast<const float*>(slice) + 2 * (g >> 1) * kSW + col;
+  float w[3][4][4];
+#pragma unroll
+  for (int c = 0; c < 3; ++c)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float2 lo = *reinterpret_cast<const float2*>(p + c * kSPlane + a * kSW);
+      const float2 hi = *reinterpret_cast<const float2*>(p + c * kSPlane + a * kSW + 2);
+      w[c][a][0] = lo.x; w[c][a][1] = lo.y; w[c][a][2] = hi.x; w[c][a][3] = hi.y;
+    }
+  __builtin_amdgcn_sched_barrier(0);
+  float f[8][4];
+  window_features(w, an, f);
   h8 hi[4], lo[4];
   feature_slices<false>(f, hi, lo);
   _Float16* feat = reinterpret_cast<_Float16*>(slice);
