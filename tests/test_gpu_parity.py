@@ -203,6 +203,35 @@ def test_tiled_equals_whole(fp16_model, R):
     assert (whole - tiled).abs().max().item() <= 2e-6
 
 
+def test_fused_path_intermediates_and_stages(mixed_model, int8_model, fp16_model):
+    """Mixed / INT8 default path: the body computes analysis + project itself, so no skip tensor exists
+    (copying it is a state error naming the flag) and the project stage reads zero; the FP16 policy
+    keeps the project kernel.  The per-layer path still exposes the skip tensor."""
+    from aeisu_amd import _lib as L
+    say("case: fused-path intermediates and stage timings (72x104)")
+    frames = _frame(72, 104, 9)[None].half().cuda().contiguous()
+    for model, on_chip in ((mixed_model, True), (int8_model, True), (fp16_model, False)):
+        hd = model.handle(1, 72, 104, torch.float16, torch.float16, L.FLAG_STAGE_TIMING)
+        model.run(frames, flags=L.FLAG_STAGE_TIMING)
+        torch.cuda.synchronize()
+        stages, n = model.stage_timings(hd)
+        say(f"  {model.precision}: stages {stages} over {n} frame(s)")
+        assert n >= 1 and stages["bottleneck"] > 0 and stages["head"] > 0
+        assert stages["compress"] == 0 and stages["expand"] == 0 and stages["refine_tail"] == 0
+        if on_chip:
+            assert stages["project"] == 0
+            with pytest.raises(L.AeisuError) as e:
+                model.intermediate(hd, L.BUF_SKIP)
+            assert e.value.code == L.AEISU_ERR_STATE and "AEISU_FLAG_UNFUSED" in str(e.value)
+            hu = model.handle(1, 72, 104, torch.float16, torch.float16, L.FLAG_UNFUSED)
+            model.run(frames, flags=L.FLAG_UNFUSED)
+            skip = model.intermediate(hu, L.BUF_SKIP)
+            assert skip.numel() == L.lib().aeisu_intermediate_bytes(hu.ptr, L.BUF_SKIP) > 0
+        else:
+            assert stages["project"] > 0
+            assert model.intermediate(hd, L.BUF_SKIP).numel() > 0
+
+
 def test_batch_and_graph_consistency(fp16_model):
     say("case: batch-2 vs per-frame, graph vs eager")
     a, b = _frame(64, 64, 21), _frame(64, 64, 22)
