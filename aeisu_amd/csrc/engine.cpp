@@ -267,7 +267,7 @@ struct Runtime {
   float analysis[24];
   float act[10] = {};
   LayerDev project, compress, grouped[4], expand, refine_tail, head;
-  DeviceBuffer compress_rgb;       // compress weights in the project-output K order (fused body, frame input)
+  DeviceBuffer compress_rgb;       // INT8 compress weights in the frame-input fused body's K order
   DeviceBuffer tail_bias;
   DeviceBuffer body_consts;        // epilogue constants of the fused body (kBodyConsts floats)
   // geometry
@@ -421,7 +421,17 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
       };
       std::function<uint32_t(int, int, int)> fn;
       int nfrag = 0;
-      if (li == 0) {
+      if (li == 0 && rt.mode == 3) {
+        // Mixed: slot s = 8g + j of phase chunk kappa takes skip channel pc(g, j) = 4g + j (j < 4) or
+        // 16 + 4g + j - 4, the project accumulator order in which the frame-input fused body holds its
+        // compress operands; every Mixed compress kernel reads in this order, so each MFMA sums its 32
+        // products in one order on every path (the FP16 MFMA's FP32 sum depends on that order)
+        nfrag = 16;
+        fn = [&](int f, int m, int s) {
+          const int g = s / 8, j = s % 8, c = j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
+          return W(16 * (f / 4) + m, c * 4 + (f % 4), 0);
+        };
+      } else if (li == 0) {
         nfrag = 16;  // f = T*4 + kappa(phase); slot s = skip channel c
         fn = [&](int f, int m, int s) { return W(16 * (f / 4) + m, s * 4 + (f % 4), 0); };
       } else if (li == 5) {
@@ -445,17 +455,6 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
         }));
       else
         dst.frag.upload(pack_frags<uint16_t>(nfrag, 8, [&](int f, int m, int s) { return (uint16_t)fn(f, m, s); }));
-      if (li == 0 && rt.mode == 3) {
-        // frame-input fused body: slot 8g + j of phase chunk kappa takes the project accumulator
-        // channel pc(g, j) = 4g + j (j < 4) or 16 + 4g + j - 4
-        auto pfn = [&](int f, int m, int s) {
-          const int g = s / 8, j = s % 8, c = j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
-          return W(16 * (f / 4) + m, c * 4 + (f % 4), 0);
-        };
-        rt.compress_rgb.upload(pack_frags<uint16_t>(16, 8, [&](int f, int m, int s) {
-          return f32_to_f16_bits(e4m3_value((uint8_t)pfn(f, m, s)));
-        }));
-      }
       if (fp8) {
         const int s_in = li == 0 ? 1 : li + 1;  // compress s1, bottleneck i s(i+2), expand s6
         const TensorView& ws = a.need(l + ".weight_scale", kF32, {cout});
@@ -673,7 +672,7 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
       P.frag[l] = layers[l]->frag.ptr;
       P.inv_out[l] = inv(rt.act[l + 2]);
     }
-    P.frag[0] = rt.compress_rgb.ptr;
+    if (m == 2) P.frag[0] = rt.compress_rgb.ptr;     // INT8: its own frame-input K order
     P.pfrag = rt.project.frag.ptr;
     P.inv_in = inv(rt.act[1]);
     P.s_out = rt.act[7];

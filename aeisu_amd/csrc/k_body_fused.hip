@@ -12,13 +12,14 @@
 // Two inputs:
 //  * BodySrc::Skip: the FP16 skip tensor written by project_kernel (per-layer-compatible path).
 //  * BodySrc::Frames16 / Frames32 (Mixed and INT8 policies): the source frames.  The kernel
-//    recomputes the analysis
-//    features and the project 1x1 for every packed pixel the compress halo needs, feeds the
-//    project accumulators to the compress MFMA as register operands (the compress weights are
-//    packed in the project-output K order), and recomputes the tile centre's skip values for
-//    the expand residual, so the 35 MB (1080p) skip tensor and its halo re-reads never touch
-//    device memory.  Features are those of features.hpp and the project arithmetic that of
-//    project_kernel, so the skip values are bit-identical.
+//    recomputes the analysis features and the project 1x1 for every packed pixel the compress
+//    halo needs, feeds the project accumulators to the compress MFMA as register operands (the
+//    compress weights are packed in the project-accumulator K order), and recomputes the tile
+//    centre's skip values for the expand residual, so the 35 MB (1080p) skip tensor and its
+//    halo re-reads never touch device memory.  Features are those of features.hpp and the
+//    project arithmetic that of project_kernel, so the skip values are bit-identical.  The FP16
+//    MFMA's FP32 sum of its 32 products depends on their order (rarely, by one ulp), so the
+//    Mixed policy's per-layer and skip-input compress read their operands in the same order.
 //
 // Arithmetic is that of the per-layer kernels in k_body.hip (same MFMA operands, same
 // epilogues), so the work tensor is bit-identical to project -> compress -> 4 x grouped ->
@@ -191,8 +192,15 @@ __device__ __forceinline__ void compress_fetch(u4 (&raw)[4], const _Float16* __r
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      raw[k] = *reinterpret_cast<const u4*>(skip + (((size_t)2 * ly + (k >> 1)) * Wq + 2 * lx + (k & 1)) * 32 + 8 * g);
+    for (int k = 0; k < 4; ++k) {
+      const _Float16* px = skip + (((size_t)2 * ly + (k >> 1)) * Wq + 2 * lx + (k & 1)) * 32;
+      if constexpr (MODE == 3) {                       // project accumulator order (see compress_kernel)
+        const u2 a = *reinterpret_cast<const u2*>(px + 4 * g), c = *reinterpret_cast<const u2*>(px + 16 + 4 * g);
+        raw[k] = u4{a[0], a[1], c[0], c[1]};
+      } else {
+        raw[k] = *reinterpret_cast<const u4*>(px + 8 * g);
+      }
+    }
   }
 }
 

@@ -36,8 +36,8 @@ hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* m
 // Input: the skip tensor (BodySrc::Skip, written by the project kernel), or (Mixed and INT8
 // policies) the frames themselves (FP16 / FP32), from which the kernel recomputes analysis features and project
 // for the compress halo and again for the expand residual, so no skip tensor exists.  The
-// frame-input variants take the compress weights in the project-output K order
-// (engine.cpp pack of compress_rgb).
+// frame-input variants take the compress weights in the project-accumulator K order: for the
+// Mixed policy every compress kernel uses that order, INT8 has a separate packing (compress_rgb).
 constexpr int kBodyConsts = 928;
 enum class BodySrc : int { Skip = 0, Frames16 = 1, Frames32 = 2 };
 struct BodyFusedArgs {

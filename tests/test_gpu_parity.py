@@ -203,6 +203,49 @@ def test_tiled_equals_whole(fp16_model, R):
     assert (whole - tiled).abs().max().item() <= 2e-6
 
 
+def test_full_size_1080p_properties(mixed_model, int8_model):
+    """BASELINE config 2 at its real size (1920x1080 -> 3840x2160, FP16 frames), checked through
+    size-independent properties: the default two-kernel path equals the per-layer path (seven kernels,
+    skip / activation / coefficient tensors in device memory) bit for bit, outputs are finite and in
+    [0, 1], a frame's result does not depend on its batch neighbours, and a flat frame reconstructs to
+    c * sum_t base[t, phase] exactly up to the FP16 output rounding (the bank has zero DC, so the
+    coefficients drop out; aeisu/reconstruction.py:68-77)."""
+    from aeisu_amd import _lib as L
+    from aeisu_amd import frames as FR
+    say("case: full-size 1080p properties")
+    scene = FR.config_frames(2).cuda().contiguous()                     # [1, 3, 1080, 1920] FP16
+    c = 0.3125
+    flat = torch.full_like(scene, c)
+    both = torch.cat([scene, flat]).contiguous()
+    for model in (mixed_model, int8_model):
+        fused = model.run(scene)
+        unfused = model.run(scene, flags=L.FLAG_UNFUSED)
+        pair = model.run(both)
+        flat_out = model.run(flat)
+        torch.cuda.synchronize()
+        say(f"  {model.precision}: max|fused - unfused| = {(fused.float() - unfused.float()).abs().max().item()}")
+        assert fused.shape == (1, 3, 2160, 3840)
+        assert torch.equal(fused, unfused)
+        assert torch.isfinite(fused.float()).all() and fused.min().item() >= 0 and fused.max().item() <= 1
+        assert torch.equal(pair[:1], fused) and torch.equal(pair[1:], flat_out)
+    # flat field against the base of the artifact the Mixed runtime loaded
+    base = _artifact_base("aeisu_area_mixed_fp8.bin")
+    out = mixed_model.run(flat).float().cpu()[0]
+    for phase in range(4):
+        i, j = phase >> 1, phase & 1
+        expect = float(np.float16(min(max(c * float(base[:, phase].astype(np.float64).sum()), 0.0), 1.0)))
+        err = (out[:, i::2, j::2] - expect).abs().max().item()
+        say(f"  flat field phase {phase}: expect {expect:.6f}, max err {err:.3g}")
+        assert err <= 2 ** -11
+
+
+def _artifact_base(name: str) -> np.ndarray:
+    """[25, 4] reconstruction base of a SPYR8F8 artifact (tap, phase)."""
+    t = spyr8f8.read_file(WEIGHTS / name)["tensors"]
+    base = np.asarray(t["adaptive_base"], dtype=np.float32)
+    return base.reshape(25, 4) if base.size == 100 else base
+
+
 def test_fused_path_intermediates_and_stages(mixed_model, int8_model, fp16_model):
     """Mixed / INT8 default path: the body computes analysis + project itself, so no skip tensor exists
     (copying it is a state error naming the flag) and the project stage reads zero; the FP16 policy
