@@ -203,7 +203,7 @@ def test_tiled_equals_whole(fp16_model, R):
     assert (whole - tiled).abs().max().item() <= 2e-6
 
 
-def test_full_size_1080p_properties(mixed_model, int8_model):
+def test_full_size_1080p_properties(mixed_model, int8_model, fp16_model, fp8mma_model):
     """BASELINE config 2 at its real size (1920x1080 -> 3840x2160, FP16 frames), checked through
     size-independent properties: the default two-kernel path equals the per-layer path (seven kernels,
     skip / activation / coefficient tensors in device memory) bit for bit, outputs are finite and in
@@ -217,7 +217,7 @@ def test_full_size_1080p_properties(mixed_model, int8_model):
     c = 0.3125
     flat = torch.full_like(scene, c)
     both = torch.cat([scene, flat]).contiguous()
-    for model in (mixed_model, int8_model):
+    for model in (mixed_model, int8_model, fp16_model, fp8mma_model):
         fused = model.run(scene)
         unfused = model.run(scene, flags=L.FLAG_UNFUSED)
         pair = model.run(both)
