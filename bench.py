@@ -101,7 +101,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-baseline work (0 = skip)")
     ap.add_argument("--graph", action="store_true",
                     help="report graph replays as the value (default: eager launches, which are faster here: "
-                         "a graph launch costs more than the three kernel launches it replaces)")
+                         "a graph launch costs more than the two or three kernel launches it replaces)")
     ap.add_argument("--unfused", action="store_true",
                     help="refine+tail and head as two kernels (coefficients through device memory)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
