@@ -281,7 +281,7 @@ struct Runtime {
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
   bool fused_rgb = false;          // the fused body takes the frames (project recomputed on chip,
-                                   // no skip tensor); Mixed and INT8 policies
+                                   // no skip tensor); the quantized policies
   bool fused_ready = false;        // fused kernels' LDS limit raised on this device
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
   // captured frame graphs, one per (input, output) buffer pair (a small LRU-free cache)
@@ -421,11 +421,11 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
       };
       std::function<uint32_t(int, int, int)> fn;
       int nfrag = 0;
-      if (li == 0 && rt.mode == 3) {
-        // Mixed: slot s = 8g + j of phase chunk kappa takes skip channel pc(g, j) = 4g + j (j < 4) or
+      if (li == 0 && (rt.mode == 1 || rt.mode == 3)) {
+        // E4M3 policies: slot s = 8g + j of phase chunk kappa takes skip channel pc(g, j) = 4g + j (j < 4) or
         // 16 + 4g + j - 4, the project accumulator order in which the frame-input fused body holds its
-        // compress operands; every Mixed compress kernel reads in this order, so each MFMA sums its 32
-        // products in one order on every path (the FP16 MFMA's FP32 sum depends on that order)
+        // compress operands; every E4M3 compress kernel reads in this order, so each MFMA sums its 32
+        // products in one order on every path (the MFMA's FP32 sum depends on that order)
         nfrag = 16;
         fn = [&](int f, int m, int s) {
           const int g = s / 8, j = s % 8, c = j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
@@ -617,7 +617,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   const size_t packed = size_t(batch) * rt.Hq * rt.Wq, lowpx = size_t(batch) * rt.Hl * rt.Wl;
   const bool fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
   // the skip tensor only exists in device memory where the project kernel runs
-  const bool fused_rgb = fused && (rt.mode == 2 || rt.mode == 3);
+  const bool fused_rgb = fused && rt.mode != 0;
   if (fused_rgb) rt.skip.release();
   else rt.skip.alloc(packed * 32 * 2);
   rt.work.alloc(packed * 32 * 2);

@@ -104,15 +104,10 @@ __global__ __launch_bounds__(256) void compress_kernel(
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const _Float16* px = skip + (((size_t)b * Hq + 2 * ly + (k >> 1)) * Wq + 2 * lxc + (k & 1)) * 32;
-        u4 raw;
-        if constexpr (MODE == 1) {
-          raw = *reinterpret_cast<const u4*>(px + 8 * g);                // K slot 8g + j = channel 8g + j
-        } else {
-          // K slot 8g + j = channel 4g + j (j < 4) or 16 + 4g + j - 4: the project accumulator order
-          // in which the frame-input fused body feeds its compress (engine.cpp packs the weights so)
-          const u2 a = *reinterpret_cast<const u2*>(px + 4 * g), c = *reinterpret_cast<const u2*>(px + 16 + 4 * g);
-          raw = u4{a[0], a[1], c[0], c[1]};
-        }
+        // K slot 8g + j = channel 4g + j (j < 4) or 16 + 4g + j - 4: the project accumulator order in
+        // which the frame-input fused body feeds its compress (engine.cpp packs the weights so)
+        const u2 a = *reinterpret_cast<const u2*>(px + 4 * g), c = *reinterpret_cast<const u2*>(px + 16 + 4 * g);
+        const u4 raw = u4{a[0], a[1], c[0], c[1]};
         const unsigned lo = pack_e4m3x4(h2f_lo_mul(raw[0], inv_in), h2f_hi_mul(raw[0], inv_in),
                                         h2f_lo_mul(raw[1], inv_in), h2f_hi_mul(raw[1], inv_in));
         const unsigned hi = pack_e4m3x4(h2f_lo_mul(raw[2], inv_in), h2f_hi_mul(raw[2], inv_in),

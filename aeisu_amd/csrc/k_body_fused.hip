@@ -11,15 +11,16 @@
 //
 // Two inputs:
 //  * BodySrc::Skip: the FP16 skip tensor written by project_kernel (per-layer-compatible path).
-//  * BodySrc::Frames16 / Frames32 (Mixed and INT8 policies): the source frames.  The kernel
+//  * BodySrc::Frames16 / Frames32 (Mixed, FP8-MFMA and INT8 policies): the source frames.  The kernel
 //    recomputes the analysis features and the project 1x1 for every packed pixel the compress
 //    halo needs, feeds the project accumulators to the compress MFMA as register operands (the
 //    compress weights are packed in the project-accumulator K order), and recomputes the tile
 //    centre's skip values for the expand residual, so the 35 MB (1080p) skip tensor and its
 //    halo re-reads never touch device memory.  Features are those of features.hpp and the
-//    project arithmetic that of project_kernel, so the skip values are bit-identical.  The FP16
-//    MFMA's FP32 sum of its 32 products depends on their order (rarely, by one ulp), so the
-//    Mixed policy's per-layer and skip-input compress read their operands in the same order.
+//    project arithmetic that of project_kernel, so the skip values are bit-identical.  The
+//    MFMA's FP32 sum of its 32 products depends on their order (the FP16 MFMA rarely, by one
+//    ulp), so the E4M3 policies' per-layer and skip-input compress read their operands in the
+//    same order.
 //
 // Arithmetic is that of the per-layer kernels in k_body.hip (same MFMA operands, same
 // epilogues), so the work tensor is bit-identical to project -> compress -> 4 x grouped ->
@@ -194,7 +195,7 @@ __device__ __forceinline__ void compress_fetch(u4 (&raw)[4], const _Float16* __r
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const _Float16* px = skip + (((size_t)2 * ly + (k >> 1)) * Wq + 2 * lx + (k & 1)) * 32;
-      if constexpr (MODE == 3) {                       // project accumulator order (see compress_kernel)
+      if constexpr (MODE == 1 || MODE == 3) {          // project accumulator order (see compress_kernel)
         const u2 a = *reinterpret_cast<const u2*>(px + 4 * g), c = *reinterpret_cast<const u2*>(px + 16 + 4 * g);
         raw[k] = u4{a[0], a[1], c[0], c[1]};
       } else {
@@ -424,7 +425,7 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
                                                 unsigned char* slice, int* counter, int wave, int lane) {
   typedef BodyFusedCfg<MODE> C;
   constexpr int S = C::S0, N = S * S, G = (N + 15) / 16, NK = C::NKc;
-  static_assert(MODE == 2 || MODE == 3, "frame input serves the Mixed and INT8 policies");
+  static_assert(MODE != 0, "frame input serves the quantized policies");
   const int g = lane >> 4;
   const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
   for (int pg = wave, next; pg < G; pg = next) {
@@ -458,7 +459,8 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
                                         h2f_hi_mul(r[1], inv_in));
         const unsigned hi = pack_e4m3x4(h2f_lo_mul(r[2], inv_in), h2f_hi_mul(r[2], inv_in), h2f_lo_mul(r[3], inv_in),
                                         h2f_hi_mul(r[3], inv_in));
-        bop = e4m3x8_to_h8(lo, hi);
+        if constexpr (MODE == 1) bop = (long)(((unsigned long)hi << 32) | lo);
+        else bop = e4m3x8_to_h8(lo, hi);
       }
 #pragma unroll
       for (int T = 0; T < 4; ++T) acc[T] = mma<MODE>(fr[(T * NK + k) * 64 + lane], bop, acc[T]);
@@ -654,7 +656,7 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   typedef BodyFusedCfg<MODE> C;
   typedef typename std::conditional<SRC == (int)BodySrc::Frames32, float, _Float16>::type Tin;
   constexpr bool RGB = SRC != (int)BodySrc::Skip;
-  static_assert(!RGB || MODE == 2 || MODE == 3, "frame input serves the Mixed and INT8 policies");
+  static_assert(!RGB || MODE != 0, "frame input serves the quantized policies (FP16 project operands)");
   static_assert(!RGB || C::Waves * kSlice <= C::SizeB, "the waves' RGB slices must fit the second buffer");
   constexpr int CPT = (kBodyConsts + C::Threads - 1) / C::Threads;   // constants per thread
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
@@ -768,11 +770,11 @@ static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&bod
 
 hipError_t body_fused_prepare() {
   const void* k[4][3] = {{body_kernel_ptr<0, 0>(), nullptr, nullptr},
-                         {body_kernel_ptr<1, 0>(), nullptr, nullptr},
+                         {body_kernel_ptr<1, 0>(), body_kernel_ptr<1, 1>(), body_kernel_ptr<1, 2>()},
                          {body_kernel_ptr<2, 0>(), body_kernel_ptr<2, 1>(), body_kernel_ptr<2, 2>()},
                          {body_kernel_ptr<3, 0>(), body_kernel_ptr<3, 1>(), body_kernel_ptr<3, 2>()}};
   const int lds[4] = {BodyFusedCfg<0>::Lds, BodyFusedCfg<1>::Lds, BodyFusedCfg<2>::Lds, BodyFusedCfg<3>::Lds};
-  const int lds_rgb[4] = {0, 0, BodyFusedCfg<2>::LdsRgb, BodyFusedCfg<3>::LdsRgb};
+  const int lds_rgb[4] = {0, BodyFusedCfg<1>::LdsRgb, BodyFusedCfg<2>::LdsRgb, BodyFusedCfg<3>::LdsRgb};
   for (int i = 0; i < 4; ++i)
     for (int j = 0; j < 3; ++j) {
       if (!k[i][j]) continue;
@@ -801,14 +803,11 @@ hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, i
   const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl);
   switch (mode) {
     case 0:
-    case 1:
-      // FP16 policy (FP16 hi/lo project operands) and FP8-MFMA variant (the FP8 MFMA's sum
-      // depends on the K order, so the permuted compress weights would not reproduce the
-      // per-layer result bit for bit): skip input only
+      // FP16 policy: skip input only (its FP16 hi/lo project operands need twice the feature slice)
       if (src != BodySrc::Skip) return hipErrorInvalidValue;
-      if (mode == 0) launch_body_t<0, 0>(args, tiles, stream);
-      else launch_body_t<1, 0>(args, tiles, stream);
+      launch_body_t<0, 0>(args, tiles, stream);
       break;
+    case 1: launch_body_m<1>(src, args, tiles, stream); break;
     case 2: launch_body_m<2>(src, args, tiles, stream); break;
     default: launch_body_m<3>(src, args, tiles, stream); break;
   }

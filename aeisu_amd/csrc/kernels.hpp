@@ -33,11 +33,11 @@ hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* m
 //   [128 + 128 l, +64) bias and [+64, +128) scale, then expand [640, 768) bias and
 //   [768, 896) scale, both indexed T * 16 + m for output channel (16 * (T >> 2) + m) * 4 + (T & 3),
 //   then the project bias [896, 928).  Scales are 0 for the FP16 policy.
-// Input: the skip tensor (BodySrc::Skip, written by the project kernel), or (Mixed and INT8
+// Input: the skip tensor (BodySrc::Skip, written by the project kernel), or (quantized
 // policies) the frames themselves (FP16 / FP32), from which the kernel recomputes analysis features and project
 // for the compress halo and again for the expand residual, so no skip tensor exists.  The
 // frame-input variants take the compress weights in the project-accumulator K order: for the
-// Mixed policy every compress kernel uses that order, INT8 has a separate packing (compress_rgb).
+// E4M3 policies every compress kernel uses that order, INT8 has a separate packing (compress_rgb).
 constexpr int kBodyConsts = 928;
 enum class BodySrc : int { Skip = 0, Frames16 = 1, Frames32 = 2 };
 struct BodyFusedArgs {

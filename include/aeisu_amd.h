@@ -56,18 +56,18 @@ extern "C" {
 
 /* intermediates for aeisu_copy_intermediate */
 #define AEISU_BUF_SKIP 0   /* FP16 [B][Hp/2][Wp/2][32] project output (not materialised on the
-                              fused path of the Mixed and INT8 policies: AEISU_ERR_STATE) */
+                              fused path of the quantized policies: AEISU_ERR_STATE) */
 #define AEISU_BUF_LOW0 1   /* [B][Hp/4][Wp/4][64] compress output (FP16 / E4M3 / INT8 codes) */
 #define AEISU_BUF_LOW4 5   /* LOW0+i: output of bottleneck i-1 (needs KEEP_INTERMEDIATES for 1..3) */
 #define AEISU_BUF_WORK 6   /* FP16 [B][Hp/2][Wp/2][32] expand + skip (refine input) */
 #define AEISU_BUF_META 7   /* FP16 [B][Hp/2][Wp/2][64] packed coefficients */
 
 /* stages reported by aeisu_stage_timings (milliseconds, averaged over recorded frames) */
-#define AEISU_STAGE_PROJECT 0      /* 0 on the fused path of the Mixed and INT8 policies (in the body) */
+#define AEISU_STAGE_PROJECT 0      /* 0 on the fused path of the quantized policies (in the body) */
 #define AEISU_STAGE_COMPRESS 1    /* 0 on the fused path (default) */
 #define AEISU_STAGE_BOTTLENECK 2  /* all four grouped layers; on the fused path the whole body
-                                     kernel (compress, bottlenecks, expand; for the Mixed and
-                                     INT8 policies also analysis + project) */
+                                     kernel (compress, bottlenecks, expand; for the quantized
+                                     policies also analysis + project) */
 #define AEISU_STAGE_EXPAND 3      /* 0 on the fused path */
 #define AEISU_STAGE_REFINE_TAIL 4 /* 0 on the fused path */
 #define AEISU_STAGE_HEAD 5        /* reconstruction head; on the fused path refine + tail + head */

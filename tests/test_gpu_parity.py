@@ -246,14 +246,14 @@ def _artifact_base(name: str) -> np.ndarray:
     return base.reshape(25, 4) if base.size == 100 else base
 
 
-def test_fused_path_intermediates_and_stages(mixed_model, int8_model, fp16_model):
-    """Mixed / INT8 default path: the body computes analysis + project itself, so no skip tensor exists
+def test_fused_path_intermediates_and_stages(mixed_model, int8_model, fp8mma_model, fp16_model):
+    """Quantized policies' default path: the body computes analysis + project itself, so no skip tensor exists
     (copying it is a state error naming the flag) and the project stage reads zero; the FP16 policy
     keeps the project kernel.  The per-layer path still exposes the skip tensor."""
     from aeisu_amd import _lib as L
     say("case: fused-path intermediates and stage timings (72x104)")
     frames = _frame(72, 104, 9)[None].half().cuda().contiguous()
-    for model, on_chip in ((mixed_model, True), (int8_model, True), (fp16_model, False)):
+    for model, on_chip in ((mixed_model, True), (int8_model, True), (fp8mma_model, True), (fp16_model, False)):
         hd = model.handle(1, 72, 104, torch.float16, torch.float16, L.FLAG_STAGE_TIMING)
         model.run(frames, flags=L.FLAG_STAGE_TIMING)
         torch.cuda.synchronize()
