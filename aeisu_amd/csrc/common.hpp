@@ -30,6 +30,16 @@ constexpr float kE4M3Max = 448.0f;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// A copy of a per-lane index that the compiler cannot see through, so addresses derived from
+// it are recomputed where they are used instead of being hoisted out of a loop or across
+// phases.  Hoisted addresses in a kernel near its register limit are spilled, and each
+// scratch reload then waits for every memory load issued before it (the memory counter
+// retires in order), which serialises prefetches.
+__device__ __forceinline__ int fresh(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ f4 mfma_f16(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

@@ -92,12 +92,27 @@ template <int MODE, int N>
 struct FragSet {
   typename BodyFusedCfg<MODE>::Frag f[N];
 };
+// Weight fragments are read with raw buffer loads: the fragment offset is a scalar and the
+// lane offset the only VGPR, so no per-fragment 64-bit address has to stay live (or be
+// spilled) between the phases that prefetch fragments and the phases that use them.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t frag_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+template <typename F>
+__device__ __forceinline__ F buffer_frag(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  if constexpr (sizeof(F) == 16) return __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  else return __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
 template <int MODE, int N>
 __device__ __forceinline__ FragSet<MODE, N> load_frags(const void* base, int first, int lane) {
-  FragSet<MODE, N> r;
+  typedef typename BodyFusedCfg<MODE>::Frag F;
+  const int f0 = __builtin_amdgcn_readfirstlane(first);   // wave-uniform
+  const __amdgpu_buffer_rsrc_t r = frag_rsrc(base, (f0 + N) * 64 * (int)sizeof(F));
+  const int voff = fresh(lane) * (int)sizeof(F);
+  FragSet<MODE, N> out;
 #pragma unroll
-  for (int i = 0; i < N; ++i) r.f[i] = reinterpret_cast<const typename BodyFusedCfg<MODE>::Frag*>(base)[(first + i) * 64 + lane];
-  return r;
+  for (int i = 0; i < N; ++i) out.f[i] = buffer_frag<F>(r, voff, (f0 + i) * 64 * (int)sizeof(F));
+  return out;
 }
 
 // Next group of a phase for this wave: the first Waves groups are dealt statically (wave w
@@ -690,12 +705,10 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   u4* fr_lds = reinterpret_cast<u4*>(bufB + C::SizeB);
   const typename C::Frag* fr = reinterpret_cast<const typename C::Frag*>(fr_lds);
   u4 fchunk[FCPT];
-  if constexpr (RGB) {
+  if constexpr (RGB) {                                 // chunks past the end read as zero
+    const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[0], C::FragBytes);
 #pragma unroll
-    for (int j = 0; j < FCPT; ++j) {
-      const int i = min(tid + j * C::Threads, FragChunks - 1);
-      fchunk[j] = reinterpret_cast<const u4*>(P.frag[0])[i];
-    }
+    for (int j = 0; j < FCPT; ++j) fchunk[j] = buffer_frag<u4>(r, tid * 16, j * C::Threads * 16);
   }
   u4 rawN[4];
   h8 pf[2];
@@ -725,11 +738,10 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   if constexpr (RGB) fb_compress_rgb<MODE, Tin>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
   else fb_compress<MODE>(P, t, bufA, cst, Fc, rawN, wave, lane);
   if constexpr (RGB) {                                 // expand weights: in flight during the barrier
+    const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[5], C::FragBytes);
+    const int voff = fresh(tid) * 16;
 #pragma unroll
-    for (int j = 0; j < FCPT; ++j) {
-      const int i = min(tid + j * C::Threads, FragChunks - 1);
-      fchunk[j] = reinterpret_cast<const u4*>(P.frag[5])[i];
-    }
+    for (int j = 0; j < FCPT; ++j) fchunk[j] = buffer_frag<u4>(r, voff, j * C::Threads * 16);
   }
   const int gf = (wave & 1) * 2 * C::NKg;              // this wave's group's first fragment
   const FragSet<MODE, 2 * C::NKg> F1 = load_frags<MODE, 2 * C::NKg>(P.frag[1], gf, lane);

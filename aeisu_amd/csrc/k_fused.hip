@@ -354,11 +354,9 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
     if (tile_of(it, G.num_tiles) >= G.num_tiles) break;   // block-uniform, as in consumer_main
     const int tn = tile_of(it + 1, G.num_tiles), tnn = tile_of(it + 2, G.num_tiles);
     const int cur = it & 1, nxt = cur ^ 1;
-    // The patch and coefficient addresses are recomputed every tile (a few VALU ops) rather
-    // than hoisted: hoisted, they are spilled to scratch, and each scratch reload waits for
-    // the patch prefetch issued before it (memory counters retire in order).
-    int ptid_it = ptid, lane_it = lane;
-    asm volatile("" : "+v"(ptid_it), "+v"(lane_it));
+    // patch and coefficient addresses are recomputed every tile (a few VALU ops); hoisted,
+    // they were spilled and their reloads waited for the patch prefetch
+    const int ptid_it = fresh(ptid), lane_it = fresh(lane);
     PatchRegs<LY> pr;
     if (tnn < G.num_tiles) patch_fetch<LY>(pr, work, fused_tile<LY::QH>(tnn, G), G, ptid_it);
     if (tn < G.num_tiles)
