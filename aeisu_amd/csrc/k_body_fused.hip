@@ -763,7 +763,13 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   fb_grouped<MODE, 4>(P, t, bufB, bufA, cst, F4, counters + 8 + (wave & 1), wave, lane);
   // frame input: the first expand group's RGB loads are issued with the expand weights (its
   // slice in the second buffer is written only after the barrier that ends the bottleneck)
-  if constexpr (RGB) stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, C::T, wave), P, lane);
+  if constexpr (RGB) {
+    stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, C::T, wave), P, fresh(lane));
+    // the project fragments are loaded again rather than kept live through the grouped layers
+    const int l = fresh(lane);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) pf[i] = reinterpret_cast<const h8*>(P.pfrag)[i * 64 + l];
+  }
   FragSet<MODE, 8 * C::NKe> Fe;
   if constexpr (!RGB) Fe = load_frags<MODE, 8 * C::NKe>(P.frag[5], 0, lane);
   lds_barrier();

@@ -224,23 +224,6 @@ __device__ __forceinline__ void rgb_store(const RgbRegs<Tin, LY>& r, Rgb* lds_rg
   }
 }
 
-// 2 FP16 coefficients (one dword) -> (u, w) with clamp(v) = u + 0.05 w, both exact in FP16
-// (identical to the head kernel's split; see k_head.hip).
-__device__ __forceinline__ void fused_clamp_split(unsigned v, unsigned& u, unsigned& w) {
-  typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-  const unsigned mag = v & 0x7FFF7FFFu;
-  const us2 m = __builtin_bit_cast(us2, mag);
-  const us2 nanpart = __builtin_elementwise_sub_sat(m, (us2){0x7C00, 0x7C00});
-  const us2 mc = __builtin_elementwise_min(m, (us2){0x4A00, 0x4A00});
-  const h2 mch = __builtin_bit_cast(h2, mc);
-  const h2 e = __builtin_elementwise_max(mch - (h2){2, 2}, (h2){0, 0});
-  const h2 um = mch - e;
-  unsigned nanbits;
-  asm("v_pk_mad_u16 %0, %1, %2, 0 clamp" : "=v"(nanbits) : "v"(__builtin_bit_cast(unsigned, nanpart)),
-      "s"(0x7E007E00u));
-  u = ((__builtin_bit_cast(unsigned, um) | nanbits) & 0x7FFF7FFFu) | (v & 0x80008000u);
-  w = (__builtin_bit_cast(unsigned, e) & 0x7FFF7FFFu) | (v & 0x80008000u);
-}
 
 // Output stores through a raw buffer resource covering one frame: lanes whose pixel lies
 // outside the frame get an offset past the range and the hardware drops their store, so
@@ -281,8 +264,8 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const int x = 2 * t.qx0 + 16 * j - G.px + n;
     const u2 coef = *reinterpret_cast<const u2*>(mrow + (8 * j + (n >> 1)) * kFMPix + 16 * (rho_y | (n & 1)) + 4 * g);
     unsigned U[2], Wd[2];
-    fused_clamp_split(coef[0], U[0], Wd[0]);
-    fused_clamp_split(coef[1], U[1], Wd[1]);
+    coef_clamp_split(coef[0], U[0], Wd[0]);
+    coef_clamp_split(coef[1], U[1], Wd[1]);
     unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
 #pragma unroll
     for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
@@ -314,18 +297,21 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     // pair phases (TL, TR) and (BL, BR): after the swap lane groups 0 and 1 both hold
     // (TL, TR), groups 2 and 3 both hold (BL, BR); groups 0 and 2 store each pair (the
     // duplicates get an out-of-range offset: identical stores would still cost write traffic)
+    // (FP16 output: the [0, 1] clamp rides on the packed convert, after the swap)
     float left[3], right[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-      left[c] = __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f);
+      left[c] = std::is_same<Tout, float>::value ? __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f) : u[c];
       right[c] = left[c];
       permlane16_swap(left[c], right[c]);
     }
     const unsigned o0 = (unsigned)(((size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x) * sizeof(Tout));
 #pragma unroll
-    for (int c = 0; c < 3; ++c)
-      fstore_pair<Tout>(ob, inside && (g & 1) == 0 ? o0 + (unsigned)(c * oplane * sizeof(Tout)) : 0xFFFFFFFFu, left[c],
-                        right[c]);
+    for (int c = 0; c < 3; ++c) {
+      const unsigned off = inside && (g & 1) == 0 ? o0 + (unsigned)(c * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
+      if constexpr (std::is_same<Tout, float>::value) fstore_pair<Tout>(ob, off, left[c], right[c]);
+      else __builtin_amdgcn_raw_buffer_store_b32(pack_h2_clamp01(left[c], right[c]), ob, (int)off, 0, 0);
+    }
   }
 }
 

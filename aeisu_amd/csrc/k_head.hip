@@ -54,21 +54,6 @@ __device__ __forceinline__ float load_px(const Tin* p) { return (float)*p; }
 
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
-// 2 FP16 coefficients (one dword) -> (u, w) with clamp(v) = u + 0.05 w, both exact in FP16.
-__device__ __forceinline__ void clamp_split(unsigned v, unsigned& u, unsigned& w) {
-  const unsigned mag = v & 0x7FFF7FFFu;
-  const us2 m = __builtin_bit_cast(us2, mag);
-  const us2 nanpart = __builtin_elementwise_sub_sat(m, (us2){0x7C00, 0x7C00});  // > 0 only for NaN
-  const us2 mc = __builtin_elementwise_min(m, (us2){0x4A00, 0x4A00});           // min(|v|, 12.0)
-  const h2 mch = __builtin_bit_cast(h2, mc);
-  const h2 e = __builtin_elementwise_max(mch - (h2){2, 2}, (h2){0, 0});          // exact
-  const h2 um = mch - e;                                                          // min(|v|, 2), exact
-  unsigned nanbits;                                                               // 0, or NaN exponent+mantissa
-  asm("v_pk_mad_u16 %0, %1, %2, 0 clamp" : "=v"(nanbits) : "v"(__builtin_bit_cast(unsigned, nanpart)),
-      "s"(0x7E007E00u));
-  u = ((__builtin_bit_cast(unsigned, um) | nanbits) & 0x7FFF7FFFu) | (v & 0x80008000u);
-  w = (__builtin_bit_cast(unsigned, e) & 0x7FFF7FFFu) | (v & 0x80008000u);
-}
 
 struct HeadTile {
   int b, y0, x0;
@@ -180,8 +165,8 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
         const int x = t.x0 + 16 * j + n;
         // coefficients 4g..4g+3 of pixel n -> (u, w) halves
         unsigned U[2], Wd[2];
-        clamp_split(coef[j][0], U[0], Wd[0]);
-        clamp_split(coef[j][1], U[1], Wd[1]);
+        coef_clamp_split(coef[j][0], U[0], Wd[0]);
+        coef_clamp_split(coef[j][1], U[1], Wd[1]);
         // u of groups 0..3 -> group g holds u[8(g&1) .. 8(g&1)+7]
         unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
 #pragma unroll
