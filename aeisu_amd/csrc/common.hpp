@@ -186,8 +186,19 @@ __device__ __forceinline__ float h2f_hi(unsigned w) {
 }
 // fl32(float(half) * s) as one v_fma_mix_f32: the FP16 operand widens exactly and adding -0
 // leaves every product (+-0 included) unchanged.
-__device__ __forceinline__ float h2f_lo_mul(unsigned w, float s) { return __builtin_fmaf(h2f_lo(w), s, -0.0f); }
-__device__ __forceinline__ float h2f_hi_mul(unsigned w, float s) { return __builtin_fmaf(h2f_hi(w), s, -0.0f); }
+// FP16 half of w times s in one v_fma_mix_f32 with a -0 addend, which equals the rounded product
+// bit for bit (x + -0 = x for every x, +0 included); the compiler turns fma(x, s, -0) into a
+// separate conversion and multiply.
+__device__ __forceinline__ float h2f_lo_mul(unsigned w, float s) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(s));
+  return r;
+}
+__device__ __forceinline__ float h2f_hi_mul(unsigned w, float s) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(s));
+  return r;
+}
 
 // Tile scheduler: the i-th tile handled by this block.  Blocks are spread
 // round-robin over the 8 XCDs; tiles are assigned so that consecutive tiles
