@@ -128,16 +128,19 @@ CONFIGS = {
 }
 
 
-def config_frames(config: int, seed: int = 0, batch: int | None = None) -> torch.Tensor:
-    """B x 3 x H x W frames of a benchmark configuration (frame i uses seed + i)."""
+def config_frames(config: int, seed: int = 0, batch: int | None = None,
+                  size: tuple[int, int] | None = None) -> torch.Tensor:
+    """B x 3 x H x W frames of a benchmark configuration (frame i uses seed + i); ``batch`` and
+    ``size`` = (H, W) override the configuration's for resolution sweeps."""
     spec = CONFIGS[config]
     n = spec["batch"] if batch is None else batch
+    h, w = (spec["height"], spec["width"]) if size is None else size
     frames = []
     for i in range(n):
         if spec["kind"] == "scene":
-            frames.append(scene(spec["height"], spec["width"], seed + i, texture=spec["texture"]))
+            frames.append(scene(h, w, seed + i, texture=spec["texture"]))
         else:
-            frames.append(pink_noise(spec["height"], spec["width"], seed + i))
+            frames.append(pink_noise(h, w, seed + i))
     out = torch.stack(frames)
     if spec["dtype"] == "fp16":
         out = out.half()

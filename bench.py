@@ -104,6 +104,11 @@ def main():
                          "a graph launch costs more than the two or three kernel launches it replaces)")
     ap.add_argument("--unfused", action="store_true",
                     help="refine+tail and head as two kernels (coefficients through device memory)")
+    ap.add_argument("--size", default=None, metavar="HxW",
+                    help="input frame size override for resolution sweeps (the headline value is config 2)")
+    ap.add_argument("--batch", type=int, default=None, help="batch override for sweeps")
+    ap.add_argument("--precision", default=None,
+                    help="precision policy override the weight file allows (fp16, mixed, mixed-fp8mma, int8)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (reference point for HBM counters)")
     args = ap.parse_args()
@@ -117,12 +122,21 @@ def main():
     from aeisu_amd import runtime as R
     from aeisu_amd import _lib as L
 
-    wl = WORKLOADS[args.config]
-    spec = FR.CONFIGS[args.config]
+    wl = dict(WORKLOADS[args.config])
+    spec = dict(FR.CONFIGS[args.config])
+    size = None
+    if args.size:
+        size = tuple(int(v) for v in args.size.lower().split("x"))
+        spec["height"], spec["width"] = size
+    if args.batch:
+        spec["batch"] = args.batch
+    if args.precision:
+        wl["precision"] = args.precision
+    sweep = bool(args.size or args.batch or args.precision)
     B, H, W = spec["batch"], spec["height"], spec["width"]
     dev = torch.device("cuda", 0)
     log(f"bench: config {args.config} ({wl['name']}), generating {args.pool} frame batches")
-    pool_cpu = [FR.config_frames(args.config, seed=1000 * i) for i in range(args.pool)]
+    pool_cpu = [FR.config_frames(args.config, seed=1000 * i, batch=B, size=size) for i in range(args.pool)]
     pool = [p.to(dev).contiguous() for p in pool_cpu]
     outs = [torch.empty(B, 3, 2 * H, 2 * W, dtype=torch.float16, device=dev) for _ in pool]
     model = R.load_model(ROOT / "weights" / wl["weights"], precision=wl["precision"])
@@ -179,11 +193,11 @@ def main():
     synth_flops = 2.0 * lr_px * 16 * 100                      # head filter synthesis (MFMA)
     # MFMA the low-precision layers run on: the Mixed policy feeds E4M3 values to the FP16 MFMA
     # (exact products, FP32 accumulation), INT8 uses the i8 MFMA
-    low_kind = {"fp16": "fp16", "mixed": "fp16", "int8": "int8"}[wl["precision"]]
+    low_kind = {"fp16": "fp16", "mixed": "fp16", "mixed-fp8mma": "fp8", "int8": "int8"}[wl["precision"]]
     ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
     ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
     fused = not args.unfused                                  # fused body and fused refine+tail+head kernels
-    traffic = measured_traffic(args.config)
+    traffic = {} if sweep else measured_traffic(args.config)   # the profile covers config 2 as defined
     kernels = {}
     proj_bytes = lr_px * 3 * s_io + packed_px * 32 * 2        # RGB in + FP16 skip out
     proj_flops = 2.0 * packed_px * 32 * 32                    # project 1x1, FP16 MFMA
@@ -259,9 +273,11 @@ def main():
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5), "ms_per_frame": round(ms_per_step / B, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": {"fp16": "fp16", "mixed": "fp8-e4m3/fp16", "int8": "int8/fp16"}[wl["precision"]],
+        "dtype": {"fp16": "fp16", "mixed": "fp8-e4m3/fp16", "mixed-fp8mma": "fp8-e4m3/fp16",
+                  "int8": "int8/fp16"}[wl["precision"]],
         "data": f"synthetic (aeisu_amd.frames config {args.config}, {args.pool} resident frames)",
-        "config": {"workload": wl["name"], "config_id": args.config, "batch": B, "input": [3, H, W],
+        "config": {"workload": wl["name"] + (" (sweep override)" if sweep else ""), "config_id": args.config,
+                   "batch": B, "input": [3, H, W],
                    "output": [3, 2 * H, 2 * W], "precision": wl["precision"], "weights": wl["weights"],
                    "timed": "graph replay" if graph else "eager launches",
                    "refine_tail_head": "two kernels" if args.unfused else "fused"},
