@@ -280,6 +280,7 @@ struct Runtime {
   int nlow = 2;
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
+  int body_tile = 0;               // side of the fused body's tile (frame input: 24, or 16 for small frames)
   bool fused_rgb = false;          // the fused body takes the frames (project recomputed on chip,
                                    // no skip tensor); the quantized policies
   bool fused_ready = false;        // fused kernels' LDS limit raised on this device
@@ -642,6 +643,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
   rt.fused = fused;
   rt.fused_rgb = fused_rgb;
+  rt.body_tile = fused_rgb ? body_fused_tile(m, batch, rt.Hl, rt.Wl, cus) : 0;
   rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
@@ -683,7 +685,7 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     P.W = rt.W;
     P.py = rt.py;
     P.px = rt.px;
-    check_hip(launch_body_fused(m, rt.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16, P, rt.batch, s),
+    check_hip(launch_body_fused(m, rt.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16, P, rt.batch, rt.body_tile, s),
               "fused body launch");
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
@@ -708,7 +710,7 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     P.s_out = m ? A[7] : 0.f;
     P.Hl = rt.Hl;
     P.Wl = rt.Wl;
-    check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, s), "fused body launch");
+    check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 0, s), "fused body launch");
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }

@@ -59,9 +59,11 @@
 
 namespace aeisu {
 
-template <int MODE>
+constexpr int kBodySliceBytes = 64 * 40 * 2;      // a wave's RGB stage / feature slice (frame input)
+
+template <int MODE, int TT = (MODE == 0 ? 16 : 24)>
 struct BodyFusedCfg {
-  static constexpr int T = MODE == 0 ? 16 : 24;     // output tile side (low pixels)
+  static constexpr int T = TT;                      // output tile side (low pixels)
   static constexpr int PIX = MODE == 0 ? 144 : 72;  // LDS bytes per pixel: 64 channels + pad
   static constexpr int S0 = T + 8;                  // compress region side
   static constexpr int SizeC = kBodyConsts * 4 + 48;   // constants + 10 group counters (+ pad)
@@ -78,7 +80,10 @@ struct BodyFusedCfg {
   static constexpr int NKe = MODE == 2 ? 1 : 2;     // expand K-chunks
   // frame input: compress, later expand, weight fragments in LDS after the second buffer
   static constexpr int FragBytes = (4 * NKc > 8 * NKe ? 4 * NKc : 8 * NKe) * 64 * (int)sizeof(Frag);
-  static constexpr int LdsRgb = Lds + FragBytes;   // used by MODE 2 and 3 only
+  // the waves' slices sit in the second buffer when it holds them (24x24 tiles), else behind the
+  // fragments (16x16 tiles)
+  static constexpr bool SlicesInB = Waves * kBodySliceBytes <= SizeB;
+  static constexpr int LdsRgb = Lds + FragBytes + (SlicesInB ? 0 : Waves * kBodySliceBytes);
 };
 
 // LDS constant table (floats), filled from BodyFusedArgs::consts.
@@ -189,10 +194,10 @@ __device__ __forceinline__ void store_act4(unsigned char* dst, typename BodyFuse
 // ---- compress: skip (HBM, FP16) -> region R0 -----------------------------------------------------
 // Skip operands of one 16-pixel group: 4 phases x 8 channels (f16 / fp8 slots) or, for INT8,
 // 2 chunks x (2 phases x 16 channels) -- raw[2k], raw[2k+1] are the two halves of chunk k.
-template <int MODE>
+template <int MODE, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void compress_fetch(u4 (&raw)[4], const _Float16* __restrict__ skip, BodyTileF t, int pg,
                                                int Hl, int Wl, int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::S0, N = S * S;
   const int n = lane & 15, g = lane >> 4, Wq = 2 * Wl;
   const int qc = min(pg * 16 + n, N - 1);
@@ -258,10 +263,10 @@ __device__ __forceinline__ void compress_mma(const u4 (&raw)[4], const FragSet<M
 }
 
 // Compress epilogue of group pg of region R0 into LDS (zero outside the low grid).
-template <int MODE>
+template <int MODE, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void compress_store(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst, const float* cst,
                                                const typename BodyFusedCfg<MODE>::Acc (&acc)[4], int pg, int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::S0, N = S * S;
   const int n = lane & 15, g = lane >> 4;
   const int q = pg * 16 + n;
@@ -278,21 +283,21 @@ __device__ __forceinline__ void compress_store(const BodyFusedArgs& P, BodyTileF
   }
 }
 
-template <int MODE>
+template <int MODE, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void fb_compress(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst, const float* cst,
                                             const FragSet<MODE, 4 * BodyFusedCfg<MODE>::NKc>& F, u4 (&rawN)[4],
                                             int wave, int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::S0, N = S * S, G = (N + 15) / 16;
   const _Float16* skip = P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32;
   for (int pg = wave; pg < G; pg += C::Waves) {
     u4 raw[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) raw[k] = rawN[k];
-    if (pg + C::Waves < G) compress_fetch<MODE>(rawN, skip, t, pg + C::Waves, P.Hl, P.Wl, lane);
+    if (pg + C::Waves < G) compress_fetch<MODE, TT>(rawN, skip, t, pg + C::Waves, P.Hl, P.Wl, lane);
     typename C::Acc acc[4];
     compress_mma<MODE>(raw, F, P.inv_in, acc);
-    compress_store<MODE>(P, t, dst, cst, acc, pg, lane);
+    compress_store<MODE, TT>(P, t, dst, cst, acc, pg, lane);
   }
 }
 
@@ -305,6 +310,7 @@ constexpr int kSW = 68, kSR = 6;                      // stage row width, rows p
 constexpr int kSPlane = kSR * kSW;                   // floats per channel
 constexpr int kFRow = 40;                            // halves per feature row (32 + 8 pad)
 constexpr int kSlice = 64 * kFRow * 2;               // bytes of a wave's slice (features >= RGB)
+static_assert(kSlice == kBodySliceBytes, "slice size");
 static_assert(3 * kSPlane * 4 <= kSlice, "RGB stage must fit the slice");
 constexpr int kStageLoads = (3 * kSPlane + 63) / 64; // staged values per lane (19 rows x 64 + rest)
 
@@ -433,12 +439,12 @@ __device__ __forceinline__ u4 project_phase(const unsigned char* slice, const h8
 
 // Frame-input compress (quantized policies).  Per group: stage -> features -> next group's RGB
 // loads issued -> per compress K-chunk, the project MFMAs of its phases and the compress MFMAs.
-template <int MODE, typename Tin>
+template <int MODE, typename Tin, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst,
                                                 const float* cst, const typename BodyFusedCfg<MODE>::Frag* fr,
                                                 const h8 (&pf)[2], const Analysis& an, RgbStage<Tin>& stN,
                                                 unsigned char* slice, int* counter, int wave, int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::S0, N = S * S, G = (N + 15) / 16, NK = C::NKc;
   static_assert(MODE != 0, "frame input serves the quantized policies");
   const int g = lane >> 4;
@@ -480,17 +486,17 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
 #pragma unroll
       for (int T = 0; T < 4; ++T) acc[T] = mma<MODE>(fr[(T * NK + k) * 64 + lane], bop, acc[T]);
     }
-    compress_store<MODE>(P, t, dst, cst, acc, pg, lane);
+    compress_store<MODE, TT>(P, t, dst, cst, acc, pg, lane);
   }
 }
 
 // ---- bottleneck L (1..4): region R(L-1) -> region RL ----------------------------------------------
-template <int MODE, int L>
+template <int MODE, int L, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void fb_grouped(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
                                            unsigned char* dst, const float* cst,
                                            const FragSet<MODE, 2 * BodyFusedCfg<MODE>::NKg>& F, int* counter, int wave,
                                            int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   typedef typename C::Acc Acc;
   constexpr int Sin = C::S0 - 2 * (L - 1), Sout = Sin - 2, N = Sout * Sout, G = (N + 15) / 16;
   constexpr int NK = C::NKg;
@@ -600,11 +606,11 @@ __device__ __forceinline__ void expand_store(const BodyFusedArgs& P, int b, int 
   }
 }
 
-template <int MODE>
+template <int MODE, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void fb_expand(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
                                           const float* cst, const FragSet<MODE, 8 * BodyFusedCfg<MODE>::NKe>& F,
                                           int wave, int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::T, N = S * S, G = (N + 15) / 16;
   const int n = lane & 15, g = lane >> 4;
   const int Hq = 2 * P.Hl, Wq = 2 * P.Wl;
@@ -623,12 +629,12 @@ __device__ __forceinline__ void fb_expand(const BodyFusedArgs& P, BodyTileF t, c
   }
 }
 
-template <int MODE, typename Tin>
+template <int MODE, typename Tin, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void fb_expand_rgb(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
                                               const float* cst, const typename BodyFusedCfg<MODE>::Frag* fr,
                                               const h8 (&pf)[2], const Analysis& an, RgbStage<Tin>& stN,
                                               unsigned char* slice, int* counter, int wave, int lane) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::T, N = S * S, G = (N + 15) / 16;
   static_assert(N % 16 == 0, "expand groups cover whole tiles");
   const int n = lane & 15, g = lane >> 4;
@@ -666,13 +672,12 @@ __device__ __forceinline__ int body_tile_of(int b, int tiles) {
   return start + (b >> 3);
 }
 
-template <int MODE, int SRC>
+template <int MODE, int SRC, int TT = BodyFusedCfg<MODE>::T>
 __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel(BodyFusedArgs P) {
-  typedef BodyFusedCfg<MODE> C;
+  typedef BodyFusedCfg<MODE, TT> C;
   typedef typename std::conditional<SRC == (int)BodySrc::Frames32, float, _Float16>::type Tin;
   constexpr bool RGB = SRC != (int)BodySrc::Skip;
   static_assert(!RGB || MODE != 0, "frame input serves the quantized policies (FP16 project operands)");
-  static_assert(!RGB || C::Waves * kSlice <= C::SizeB, "the waves' RGB slices must fit the second buffer");
   constexpr int CPT = (kBodyConsts + C::Threads - 1) / C::Threads;   // constants per thread
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* cst = reinterpret_cast<float*>(smem);
@@ -681,7 +686,7 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   unsigned char* bufA = smem + C::SizeC;
   unsigned char* bufB = bufA + C::SizeA;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  unsigned char* slice = bufB + wave * kSlice;       // frame input: this wave's RGB / feature slice
+  unsigned char* slice = (C::SlicesInB ? bufB : bufB + C::SizeB + C::FragBytes) + wave * kSlice;   // frame input
   const int tx = (P.Wl + C::T - 1) / C::T, ty = (P.Hl + C::T - 1) / C::T;
   const int tidx = body_tile_of((int)blockIdx.x, (int)gridDim.x);
   BodyTileF t;
@@ -721,7 +726,7 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
     an = analysis_from(P.analysis);
     stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, C::S0, wave), P, lane);
   } else {
-    compress_fetch<MODE>(rawN, P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32, t, wave, P.Hl, P.Wl, lane);
+    compress_fetch<MODE, TT>(rawN, P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32, t, wave, P.Hl, P.Wl, lane);
   }
 #pragma unroll
   for (int j = 0; j < CPT; ++j) {
@@ -735,8 +740,8 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   }
   if (tid < 10) counters[tid] = tid < 2 ? C::Waves : C::Waves / 2;
   lds_barrier();
-  if constexpr (RGB) fb_compress_rgb<MODE, Tin>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
-  else fb_compress<MODE>(P, t, bufA, cst, Fc, rawN, wave, lane);
+  if constexpr (RGB) fb_compress_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
+  else fb_compress<MODE, TT>(P, t, bufA, cst, Fc, rawN, wave, lane);
   if constexpr (RGB) {                                 // expand weights: in flight during the barrier
     const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[5], C::FragBytes);
     const int voff = fresh(tid) * 16;
@@ -751,16 +756,16 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
     for (int j = 0; j < FCPT; ++j)
       if (tid + j * C::Threads < FragChunks) fr_lds[tid + j * C::Threads] = fchunk[j];
   }
-  fb_grouped<MODE, 1>(P, t, bufA, bufB, cst, F1, counters + 2 + (wave & 1), wave, lane);
+  fb_grouped<MODE, 1, TT>(P, t, bufA, bufB, cst, F1, counters + 2 + (wave & 1), wave, lane);
   const FragSet<MODE, 2 * C::NKg> F2 = load_frags<MODE, 2 * C::NKg>(P.frag[2], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 2>(P, t, bufB, bufA, cst, F2, counters + 4 + (wave & 1), wave, lane);
+  fb_grouped<MODE, 2, TT>(P, t, bufB, bufA, cst, F2, counters + 4 + (wave & 1), wave, lane);
   const FragSet<MODE, 2 * C::NKg> F3 = load_frags<MODE, 2 * C::NKg>(P.frag[3], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 3>(P, t, bufA, bufB, cst, F3, counters + 6 + (wave & 1), wave, lane);
+  fb_grouped<MODE, 3, TT>(P, t, bufA, bufB, cst, F3, counters + 6 + (wave & 1), wave, lane);
   const FragSet<MODE, 2 * C::NKg> F4 = load_frags<MODE, 2 * C::NKg>(P.frag[4], gf, lane);
   lds_barrier();
-  fb_grouped<MODE, 4>(P, t, bufB, bufA, cst, F4, counters + 8 + (wave & 1), wave, lane);
+  fb_grouped<MODE, 4, TT>(P, t, bufB, bufA, cst, F4, counters + 8 + (wave & 1), wave, lane);
   // frame input: the first expand group's RGB loads are issued with the expand weights (its
   // slice in the second buffer is written only after the barrier that ends the bottleneck)
   if constexpr (RGB) {
@@ -773,61 +778,88 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   FragSet<MODE, 8 * C::NKe> Fe;
   if constexpr (!RGB) Fe = load_frags<MODE, 8 * C::NKe>(P.frag[5], 0, lane);
   lds_barrier();
-  if constexpr (RGB) fb_expand_rgb<MODE, Tin>(P, t, bufA, cst, fr, pf, an, stN, slice, counters + 1, wave, lane);
-  else fb_expand<MODE>(P, t, bufA, cst, Fe, wave, lane);
+  if constexpr (RGB) fb_expand_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters + 1, wave, lane);
+  else fb_expand<MODE, TT>(P, t, bufA, cst, Fe, wave, lane);
 }
 
 // ------------------------------------------------------------------------------------------------
-int body_fused_num_tiles(int mode, int batch, int Hl, int Wl) {
-  const int T = mode == 0 ? BodyFusedCfg<0>::T : BodyFusedCfg<3>::T;
+int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile) {
+  const int T = tile ? tile : (mode == 0 ? BodyFusedCfg<0>::T : BodyFusedCfg<3>::T);
   return batch * ((Hl + T - 1) / T) * ((Wl + T - 1) / T);
 }
 
-template <int MODE, int SRC>
-static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&body_fused_kernel<MODE, SRC>); }
+// Tile side for a frame-input launch: a block computes one tile, so the body takes
+// ceil(tiles / CUs) tile-times.  A 16x16 tile costs about 0.6 of a 24x24 one (its compress region
+// is 24^2 against 32^2 pixels, bottleneck and expand regions shrink alike), so small frames
+// (one round either way) take 16x16 tiles and large frames and batches 24x24 ones.
+int body_fused_tile(int mode, int batch, int Hl, int Wl, int cus) {
+  if (mode == 0 || cus <= 0) return mode == 0 ? BodyFusedCfg<0>::T : BodyFusedCfg<3>::T;
+  const long r24 = (body_fused_num_tiles(mode, batch, Hl, Wl, 24) + cus - 1) / cus;
+  const long r16 = (body_fused_num_tiles(mode, batch, Hl, Wl, 16) + cus - 1) / cus;
+  return 6 * r16 < 10 * r24 ? 16 : 24;                 // 0.6 r16 < r24
+}
+
+template <int MODE, int SRC, int TT>
+static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&body_fused_kernel<MODE, SRC, TT>); }
 
 hipError_t body_fused_prepare() {
-  const void* k[4][3] = {{body_kernel_ptr<0, 0>(), nullptr, nullptr},
-                         {body_kernel_ptr<1, 0>(), body_kernel_ptr<1, 1>(), body_kernel_ptr<1, 2>()},
-                         {body_kernel_ptr<2, 0>(), body_kernel_ptr<2, 1>(), body_kernel_ptr<2, 2>()},
-                         {body_kernel_ptr<3, 0>(), body_kernel_ptr<3, 1>(), body_kernel_ptr<3, 2>()}};
-  const int lds[4] = {BodyFusedCfg<0>::Lds, BodyFusedCfg<1>::Lds, BodyFusedCfg<2>::Lds, BodyFusedCfg<3>::Lds};
-  const int lds_rgb[4] = {0, BodyFusedCfg<1>::LdsRgb, BodyFusedCfg<2>::LdsRgb, BodyFusedCfg<3>::LdsRgb};
-  for (int i = 0; i < 4; ++i)
-    for (int j = 0; j < 3; ++j) {
-      if (!k[i][j]) continue;
-      const hipError_t e =
-          hipFuncSetAttribute(k[i][j], hipFuncAttributeMaxDynamicSharedMemorySize, j ? lds_rgb[i] : lds[i]);
-      if (e != hipSuccess) return e;
-    }
+  struct K {
+    const void* fn;
+    int lds;
+  };
+  const K k[] = {
+      {body_kernel_ptr<0, 0, 16>(), BodyFusedCfg<0>::Lds},
+      {body_kernel_ptr<1, 0, 24>(), BodyFusedCfg<1>::Lds},        {body_kernel_ptr<2, 0, 24>(), BodyFusedCfg<2>::Lds},
+      {body_kernel_ptr<3, 0, 24>(), BodyFusedCfg<3>::Lds},
+      {body_kernel_ptr<1, 1, 24>(), BodyFusedCfg<1, 24>::LdsRgb}, {body_kernel_ptr<1, 2, 24>(), BodyFusedCfg<1, 24>::LdsRgb},
+      {body_kernel_ptr<2, 1, 24>(), BodyFusedCfg<2, 24>::LdsRgb}, {body_kernel_ptr<2, 2, 24>(), BodyFusedCfg<2, 24>::LdsRgb},
+      {body_kernel_ptr<3, 1, 24>(), BodyFusedCfg<3, 24>::LdsRgb}, {body_kernel_ptr<3, 2, 24>(), BodyFusedCfg<3, 24>::LdsRgb},
+      {body_kernel_ptr<1, 1, 16>(), BodyFusedCfg<1, 16>::LdsRgb}, {body_kernel_ptr<1, 2, 16>(), BodyFusedCfg<1, 16>::LdsRgb},
+      {body_kernel_ptr<2, 1, 16>(), BodyFusedCfg<2, 16>::LdsRgb}, {body_kernel_ptr<2, 2, 16>(), BodyFusedCfg<2, 16>::LdsRgb},
+      {body_kernel_ptr<3, 1, 16>(), BodyFusedCfg<3, 16>::LdsRgb}, {body_kernel_ptr<3, 2, 16>(), BodyFusedCfg<3, 16>::LdsRgb}};
+  for (const K& e : k) {
+    const hipError_t r = hipFuncSetAttribute(e.fn, hipFuncAttributeMaxDynamicSharedMemorySize, e.lds);
+    if (r != hipSuccess) return r;
+  }
   return hipSuccess;
 }
 
-template <int MODE, int SRC>
+template <int MODE, int SRC, int TT>
 static void launch_body_t(const BodyFusedArgs& args, int tiles, hipStream_t stream) {
-  hipLaunchKernelGGL((body_fused_kernel<MODE, SRC>), dim3(tiles), dim3(BodyFusedCfg<MODE>::Threads),
-                     SRC ? BodyFusedCfg<MODE>::LdsRgb : BodyFusedCfg<MODE>::Lds, stream, args);
+  typedef BodyFusedCfg<MODE, TT> C;
+  constexpr int lds = SRC ? C::LdsRgb : C::Lds;
+  hipLaunchKernelGGL((body_fused_kernel<MODE, SRC, TT>), dim3(tiles), dim3(C::Threads), lds, stream, args);
 }
 template <int MODE>
-static void launch_body_m(BodySrc src, const BodyFusedArgs& args, int tiles, hipStream_t stream) {
+static void launch_body_m(BodySrc src, const BodyFusedArgs& args, int tile, int tiles, hipStream_t stream) {
   switch (src) {
-    case BodySrc::Skip: launch_body_t<MODE, 0>(args, tiles, stream); break;
-    case BodySrc::Frames16: launch_body_t<MODE, 1>(args, tiles, stream); break;
-    default: launch_body_t<MODE, 2>(args, tiles, stream); break;
+    case BodySrc::Skip: launch_body_t<MODE, 0, 24>(args, tiles, stream); break;
+    case BodySrc::Frames16:
+      if (tile == 16) launch_body_t<MODE, 1, 16>(args, tiles, stream);
+      else launch_body_t<MODE, 1, 24>(args, tiles, stream);
+      break;
+    default:
+      if (tile == 16) launch_body_t<MODE, 2, 16>(args, tiles, stream);
+      else launch_body_t<MODE, 2, 24>(args, tiles, stream);
+      break;
   }
 }
 
-hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, hipStream_t stream) {
-  const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl);
+hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
+                             hipStream_t stream) {
+  if (mode == 0) {
+    // FP16 policy: skip input only (its FP16 hi/lo project operands need twice the feature slice)
+    if (src != BodySrc::Skip || (tile && tile != 16)) return hipErrorInvalidValue;
+    launch_body_t<0, 0, 16>(args, body_fused_num_tiles(0, batch, args.Hl, args.Wl, 16), stream);
+    return hipGetLastError();
+  }
+  if (tile == 0) tile = 24;
+  if (tile != 24 && (tile != 16 || src == BodySrc::Skip)) return hipErrorInvalidValue;
+  const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl, tile);
   switch (mode) {
-    case 0:
-      // FP16 policy: skip input only (its FP16 hi/lo project operands need twice the feature slice)
-      if (src != BodySrc::Skip) return hipErrorInvalidValue;
-      launch_body_t<0, 0>(args, tiles, stream);
-      break;
-    case 1: launch_body_m<1>(src, args, tiles, stream); break;
-    case 2: launch_body_m<2>(src, args, tiles, stream); break;
-    default: launch_body_m<3>(src, args, tiles, stream); break;
+    case 1: launch_body_m<1>(src, args, tile, tiles, stream); break;
+    case 2: launch_body_m<2>(src, args, tile, tiles, stream); break;
+    default: launch_body_m<3>(src, args, tile, tiles, stream); break;
   }
   return hipGetLastError();
 }

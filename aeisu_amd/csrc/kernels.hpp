@@ -54,9 +54,13 @@ struct BodyFusedArgs {
   int Hl, Wl;
   int H, W, py, px;        // frame geometry (frame-input variants)
 };
-int body_fused_num_tiles(int mode, int batch, int Hl, int Wl);
+// tile = side of the body's output tile in low pixels (0: the policy's default, 24, or 16 for the FP16 policy)
+int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile = 0);
+// tile side for a frame-input launch on a device with `cus` compute units (16 or 24)
+int body_fused_tile(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();
-hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, hipStream_t stream);
+hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
+                             hipStream_t stream);
 
 // Fused refine + tail + head (coefficients in LDS); one block per CU (1024 threads for FP16
 // frames, 768 for FP32 frames).
