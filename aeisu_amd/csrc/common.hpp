@@ -28,6 +28,10 @@ typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u2 __attribute__((ext_vector_type(2)));
 
 constexpr float kE4M3Max = 448.0f;
+// Word 3 of a raw (untyped, stride 0) buffer resource: DATA_FORMAT = 32 bit (bits 18:15 = 4), the
+// only field untyped loads and stores need non-zero; offsets at or past num_records are dropped
+// on stores and read as zero on loads.
+constexpr int kRawBufferWord3 = 0x00020000;
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 

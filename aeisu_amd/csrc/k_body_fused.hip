@@ -101,7 +101,7 @@ struct FragSet {
 // lane offset the only VGPR, so no per-fragment 64-bit address has to stay live (or be
 // spilled) between the phases that prefetch fragments and the phases that use them.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t frag_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRawBufferWord3);
 }
 template <typename F>
 __device__ __forceinline__ F buffer_frag(__amdgpu_buffer_rsrc_t r, int voff, int soff) {

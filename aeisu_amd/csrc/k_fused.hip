@@ -230,7 +230,7 @@ __device__ __forceinline__ void rgb_store(const RgbRegs<Tin, LY>& r, Rgb* lds_rg
 // the stores need no branch (raw-buffer range checking: offset >= num_records is not
 // written).  A frame is at most 3 x 8192^2 x 4 x 4 bytes < 2^32.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t frame_rsrc(void* base, size_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(unsigned)bytes, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)(unsigned)bytes, kRawBufferWord3);
 }
 template <typename Tout>
 __device__ __forceinline__ void fstore_pair(__amdgpu_buffer_rsrc_t r, unsigned off, float left, float right);

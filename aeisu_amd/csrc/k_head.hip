@@ -52,8 +52,6 @@ constexpr int kHeadFragBytes = 7 * 64 * 16 + 14 * 64 * 8;
 template <typename Tin>
 __device__ __forceinline__ float load_px(const Tin* p) { return (float)*p; }
 
-typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-
 
 struct HeadTile {
   int b, y0, x0;
