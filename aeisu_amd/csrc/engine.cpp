@@ -584,7 +584,8 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   if ((in_layout != AEISU_LAYOUT_NCHW_F16 && in_layout != AEISU_LAYOUT_NCHW_F32) ||
       (out_layout != AEISU_LAYOUT_NCHW_F16 && out_layout != AEISU_LAYOUT_NCHW_F32))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unsupported frame layout");
-  if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD | AEISU_FLAG_UNFUSED))
+  if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD | AEISU_FLAG_UNFUSED |
+                AEISU_FLAG_BODY_TILE24))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unknown configure flag");
   const bool no_pad = flags & AEISU_FLAG_NO_PAD;
   if (no_pad && (height % 4 || width % 4))
@@ -643,7 +644,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
   rt.fused = fused;
   rt.fused_rgb = fused_rgb;
-  rt.body_tile = fused_rgb ? body_fused_tile(m, batch, rt.Hl, rt.Wl, cus) : 0;
+  rt.body_tile = !fused_rgb ? 0 : (flags & AEISU_FLAG_BODY_TILE24) ? 24 : body_fused_tile(m, batch, rt.Hl, rt.Wl, cus);
   rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");

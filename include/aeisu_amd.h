@@ -53,6 +53,8 @@ extern "C" {
                                             coefficient tensor in device memory (the reference
                                             engine's structure); default: one fused kernel, the
                                             coefficients stay on chip.  KEEP_INTERMEDIATES implies it */
+#define AEISU_FLAG_BODY_TILE24 16u       /* frame-input body: always 24x24-low-pixel tiles (by default small
+                                            frames take 16x16 tiles; parity tests run both) */
 
 /* intermediates for aeisu_copy_intermediate */
 #define AEISU_BUF_SKIP 0   /* FP16 [B][Hp/2][Wp/2][32] project output (not materialised on the

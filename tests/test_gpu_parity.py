@@ -112,18 +112,20 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
     """Same arithmetic, same rounding points: the fused body kernel and the fused refine+tail+head kernel
     must reproduce the per-layer path bit for bit in every policy, including odd padding offsets
     (70x102 -> py = px = 29), frames narrower than one tile row and low grids that are not a multiple
-    of the body tile (37x333, 200x72 in a batch of 3)."""
+    of the body tile (37x333, 200x72 in a batch of 3), with the body tile these shapes select (16x16 for
+    the quantized policies) and with 24x24 tiles forced."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
     frames = torch.stack([_frame(h, w, 40 + i) for i in range(b)]).to(dt).cuda().contiguous()
     for model in (mixed_model, fp16_model, int8_model, fp8mma_model):
-        fused = model.run(frames)
         unfused = model.run(frames, flags=L.FLAG_UNFUSED)
-        torch.cuda.synchronize()
-        diff = (fused.float() - unfused.float()).abs().max().item()
-        say(f"  {model.precision}: max|fused - unfused| = {diff}")
-        assert torch.equal(fused, unfused)
+        for flags, tile in ((0, "shape's tile"), (L.FLAG_BODY_TILE24, "24x24 tiles")):
+            fused = model.run(frames, flags=flags)
+            torch.cuda.synchronize()
+            diff = (fused.float() - unfused.float()).abs().max().item()
+            say(f"  {model.precision} ({tile}): max|fused - unfused| = {diff}")
+            assert torch.equal(fused, unfused)
 
 
 # ------------------------------------------------------------------------------------------------
