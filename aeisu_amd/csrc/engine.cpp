@@ -280,7 +280,7 @@ struct Runtime {
   int nlow = 2;
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
-  int body_tile = 0;               // side of the fused body's tile (frame input: 24, or 16 for small frames)
+  int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
   bool fused_rgb = false;          // the fused body takes the frames (project recomputed on chip,
                                    // no skip tensor); the quantized policies
   bool fused_ready = false;        // fused kernels' LDS limit raised on this device
@@ -644,7 +644,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
   rt.fused = fused;
   rt.fused_rgb = fused_rgb;
-  rt.body_tile = !fused_rgb ? 0 : (flags & AEISU_FLAG_BODY_TILE24) ? 24 : body_fused_tile(m, batch, rt.Hl, rt.Wl, cus);
+  rt.body_split = (flags & AEISU_FLAG_BODY_TILE24) ? batch : body_fused_split(m, batch, rt.Hl, rt.Wl, cus);
   rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
@@ -686,8 +686,15 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     P.W = rt.W;
     P.py = rt.py;
     P.px = rt.px;
-    check_hip(launch_body_fused(m, rt.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16, P, rt.batch, rt.body_tile, s),
-              "fused body launch");
+    const BodySrc src = rt.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
+    const int k = rt.body_split;
+    if (k > 0) check_hip(launch_body_fused(m, src, P, k, 24, s), "fused body launch");
+    if (k < rt.batch) {                            // trailing frames on 16x16 tiles
+      BodyFusedArgs Q = P;
+      Q.frames = static_cast<const char*>(P.frames) + size_t(k) * 3 * rt.H * rt.W * (rt.in_fp32 ? 4 : 2);
+      Q.work = P.work + size_t(k) * rt.Hq * rt.Wq * 32;
+      check_hip(launch_body_fused(m, src, Q, rt.batch - k, 16, s), "fused body launch");
+    }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }

@@ -788,15 +788,26 @@ int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile) {
   return batch * ((Hl + T - 1) / T) * ((Wl + T - 1) / T);
 }
 
-// Tile side for a frame-input launch: a block computes one tile, so the body takes
-// ceil(tiles / CUs) tile-times.  A 16x16 tile costs about 0.6 of a 24x24 one (its compress region
-// is 24^2 against 32^2 pixels, bottleneck and expand regions shrink alike), so small frames
-// (one round either way) take 16x16 tiles and large frames and batches 24x24 ones.
-int body_fused_tile(int mode, int batch, int Hl, int Wl, int cus) {
-  if (mode == 0 || cus <= 0) return mode == 0 ? BodyFusedCfg<0>::T : BodyFusedCfg<3>::T;
-  const long r24 = (body_fused_num_tiles(mode, batch, Hl, Wl, 24) + cus - 1) / cus;
-  const long r16 = (body_fused_num_tiles(mode, batch, Hl, Wl, 16) + cus - 1) / cus;
-  return 6 * r16 < 10 * r24 ? 16 : 24;                 // 0.6 r16 < r24
+// Frame-input tiles: a block computes one tile, so a launch takes ceil(tiles / CUs) tile-times, and a
+// 16x16 tile costs about 0.6 of a 24x24 one (its compress region is 24^2 against 32^2 pixels, the
+// bottleneck and expand regions shrink alike).  The batch is split into leading frames on 24x24
+// tiles and trailing frames on 16x16 tiles (two launches), at the split with the fewest weighted
+// rounds: small frames at batch 1 take 16x16 tiles, 1080p and larger 24x24 ones, and a batch whose
+// 24x24 tiles leave a nearly empty last round (540p x 8) moves its last frame to 16x16 tiles.
+// Returns the number of frames on 24x24 tiles.
+int body_fused_split(int mode, int batch, int Hl, int Wl, int cus) {
+  if (mode == 0 || cus <= 0) return batch;
+  const long t24 = body_fused_num_tiles(mode, 1, Hl, Wl, 24), t16 = body_fused_num_tiles(mode, 1, Hl, Wl, 16);
+  long best = -1;
+  int best_k = batch;
+  for (int k = batch; k >= 0; --k) {             // ties keep more frames on 24x24 tiles
+    const long cost = 10 * ((t24 * k + cus - 1) / cus) + 6 * ((t16 * (batch - k) + cus - 1) / cus);
+    if (best < 0 || cost < best) {
+      best = cost;
+      best_k = k;
+    }
+  }
+  return best_k;
 }
 
 template <int MODE, int SRC, int TT>

@@ -56,8 +56,9 @@ struct BodyFusedArgs {
 };
 // tile = side of the body's output tile in low pixels (0: the policy's default, 24, or 16 for the FP16 policy)
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile = 0);
-// tile side for a frame-input launch on a device with `cus` compute units (16 or 24)
-int body_fused_tile(int mode, int batch, int Hl, int Wl, int cus);
+// frame-input body: how many leading frames of a batch run on 24x24 tiles (the rest on 16x16 tiles)
+// on a device with `cus` compute units
+int body_fused_split(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();
 hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
                              hipStream_t stream);

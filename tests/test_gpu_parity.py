@@ -107,13 +107,14 @@ def test_head_phase_packing_exact(fp16_model, area_state):
 # fused kernels (body activations and coefficients on chip) vs the per-layer path
 # ------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("h,w,b,fp32", [(72, 104, 1, False), (70, 102, 2, True), (37, 333, 1, False),
-                                         (540, 960, 1, False), (200, 72, 3, False)])
+                                         (540, 960, 1, False), (200, 72, 3, False), (540, 960, 8, False)])
 def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model, h, w, b, fp32):
     """Same arithmetic, same rounding points: the fused body kernel and the fused refine+tail+head kernel
     must reproduce the per-layer path bit for bit in every policy, including odd padding offsets
     (70x102 -> py = px = 29), frames narrower than one tile row and low grids that are not a multiple
-    of the body tile (37x333, 200x72 in a batch of 3), with the body tile these shapes select (16x16 for
-    the quantized policies) and with 24x24 tiles forced."""
+    of the body tile (37x333, 200x72 in a batch of 3), with the body tiles these shapes select (16x16 for
+    the small frames; 540p x 8 splits into 7 frames on 24x24 and 1 on 16x16 tiles, two launches) and with
+    24x24 tiles forced."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
