@@ -33,7 +33,9 @@
 // flattened and cut into 16-pixel MFMA column groups, so no MFMA work is lost to row ends.
 //  * byte activations (E4M3 codes, INT8): T = 24 (252 tiles at 1080p, one per CU), 72 bytes
 //    per LDS pixel; the Mixed policy widens codes to FP16 operands with
-//    v_cvt_scalef32_pk_f16_fp8 as it reads them.
+//    v_cvt_scalef32_pk_f16_fp8 as it reads them.  The frame-input variants also come with
+//    T = 16 for frames whose 24x24 tiles would leave CUs idle (body_fused_split picks the
+//    tile per batch, possibly two launches: leading frames on 24x24, trailing on 16x16 tiles).
 //  * FP16 activations: T = 16, 144 bytes per LDS pixel.
 // 12 waves (3 per SIMD, up to 168 VGPRs each): compress and expand split the pixel groups over
 // all waves; in a grouped layer, wave w serves group w & 1 and keeps that group's 18 weight
@@ -42,7 +44,8 @@
 // Frame input, per 16-low-pixel group (64 packed pixels, one per lane): the wave stages the
 // group's RGB (6 LR rows x up to 68 columns per channel: one or two row segments when the
 // group wraps a region row) in its own 5 KB LDS slice -- the slices live in the second
-// activation buffer, which is free during compress and expand -- with the next group's RGB in
+// activation buffer, which is free during compress and expand (T = 24), or behind the weight
+// fragments where that buffer is too small for them (T = 16) -- with the next group's RGB in
 // flight in registers.  Each lane computes the 32 features of one packed pixel into the slice
 // (over the RGB: a wave's LDS operations execute in order), the project MFMA reads them back
 // as operands, and its accumulators become the skip operands.  No workgroup barrier is needed
@@ -50,7 +53,9 @@
 //
 // Latency: the layers hand over through LDS only, so the barrier between layers waits for LDS
 // (lgkmcnt) and not for global loads; each wave issues the next layer's weight fragments
-// before the barrier.  Compress prefetches the operands of its next pixel group, expand
+// (raw buffer loads: a scalar offset per fragment, so no address has to survive in a VGPR)
+// before the barrier.  The kernel must not spill: a scratch reload waits for every memory load
+// issued before it, which would serialise these prefetches.  Compress prefetches the operands of its next pixel group, expand
 // issues its global loads before the MFMAs.  Blocks are mapped to tiles in XCD bands, so the
 // tiles whose compress halos overlap run in the same L2.
 #include "common.hpp"
