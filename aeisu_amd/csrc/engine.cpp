@@ -281,6 +281,7 @@ struct Runtime {
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
   int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
+  int body_rows16 = 0;             // FP16 policy body: low rows on 16x16 tiles, the rest on 8x8
   bool fused_rgb = false;          // the fused body takes the frames (project recomputed on chip,
                                    // no skip tensor); the quantized policies
   bool fused_ready = false;        // fused kernels' LDS limit raised on this device
@@ -645,6 +646,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.fused = fused;
   rt.fused_rgb = fused_rgb;
   rt.body_split = (flags & AEISU_FLAG_BODY_TILE24) ? batch : body_fused_split(m, batch, rt.Hl, rt.Wl, cus);
+  rt.body_rows16 = (flags & AEISU_FLAG_BODY_TILE24) ? rt.Hl : body_fused_row_split(m, batch, rt.Hl, rt.Wl, cus);
   rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
   if (rt.fused && !rt.fused_ready) {
     check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
@@ -718,7 +720,18 @@ static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_
     P.s_out = m ? A[7] : 0.f;
     P.Hl = rt.Hl;
     P.Wl = rt.Wl;
-    check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 0, s), "fused body launch");
+    if (m != 0 || rt.body_rows16 >= rt.Hl) {
+      check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 0, s), "fused body launch");
+    } else {                                       // FP16 policy: bottom rows on 8x8 tiles
+      if (rt.body_rows16 > 0) {
+        P.row0 = 0;
+        P.rows = rt.body_rows16;
+        check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 16, s), "fused body launch");
+      }
+      P.row0 = rt.body_rows16;
+      P.rows = rt.Hl - rt.body_rows16;
+      check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 8, s), "fused body launch");
+    }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }

@@ -692,12 +692,12 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   unsigned char* bufB = bufA + C::SizeA;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   unsigned char* slice = (C::SlicesInB ? bufB : bufB + C::SizeB + C::FragBytes) + wave * kSlice;   // frame input
-  const int tx = (P.Wl + C::T - 1) / C::T, ty = (P.Hl + C::T - 1) / C::T;
+  const int tx = (P.Wl + C::T - 1) / C::T, ty = ((P.rows ? P.rows : P.Hl) + C::T - 1) / C::T;
   const int tidx = body_tile_of((int)blockIdx.x, (int)gridDim.x);
   BodyTileF t;
   t.b = tidx / (tx * ty);
   const int rem = tidx - t.b * tx * ty;
-  t.y0 = (rem / tx) * C::T;
+  t.y0 = P.row0 + (rem / tx) * C::T;
   t.x0 = (rem % tx) * C::T;
   // constants, compress weights and the first group's operands are in flight together
   float cv[CPT];
@@ -815,6 +815,28 @@ int body_fused_split(int mode, int batch, int Hl, int Wl, int cus) {
   return best_k;
 }
 
+// FP16 policy: the same trade between 16x16 tiles and 8x8 tiles (compress region 16^2 against
+// 24^2 pixels plus the fixed per-tile prologue: about half the cost), split by low rows since the
+// batch is usually one frame.  1080p: 18 rows of 31 tiles (558) take three rounds of which the
+// last holds 46 tiles; rows 0-255 on 16x16 tiles (496, two rounds) and 256-279 on 8x8 tiles (183,
+// one round) take 2.5 tile-times.
+int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus) {
+  if (mode != 0 || cus <= 0) return Hl;
+  const int top = (Hl + 15) / 16 * 16;
+  long best = -1;
+  int best_r = top;
+  for (int r = top; r >= 0; r -= 16) {            // ties keep more rows on 16x16 tiles
+    const long t16 = (long)batch * ((r + 15) / 16) * ((Wl + 15) / 16);
+    const long t8 = r >= Hl ? 0 : (long)batch * ((Hl - r + 7) / 8) * ((Wl + 7) / 8);
+    const long cost = 10 * ((t16 + cus - 1) / cus) + 5 * ((t8 + cus - 1) / cus);
+    if (best < 0 || cost < best) {
+      best = cost;
+      best_r = r;
+    }
+  }
+  return best_r >= Hl ? Hl : best_r;
+}
+
 template <int MODE, int SRC, int TT>
 static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&body_fused_kernel<MODE, SRC, TT>); }
 
@@ -824,7 +846,7 @@ hipError_t body_fused_prepare() {
     int lds;
   };
   const K k[] = {
-      {body_kernel_ptr<0, 0, 16>(), BodyFusedCfg<0>::Lds},
+      {body_kernel_ptr<0, 0, 16>(), BodyFusedCfg<0>::Lds},     {body_kernel_ptr<0, 0, 8>(), BodyFusedCfg<0, 8>::Lds},
       {body_kernel_ptr<1, 0, 24>(), BodyFusedCfg<1>::Lds},        {body_kernel_ptr<2, 0, 24>(), BodyFusedCfg<2>::Lds},
       {body_kernel_ptr<3, 0, 24>(), BodyFusedCfg<3>::Lds},
       {body_kernel_ptr<1, 1, 24>(), BodyFusedCfg<1, 24>::LdsRgb}, {body_kernel_ptr<1, 2, 24>(), BodyFusedCfg<1, 24>::LdsRgb},
@@ -863,15 +885,20 @@ static void launch_body_m(BodySrc src, const BodyFusedArgs& args, int tile, int 
 
 hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
                              hipStream_t stream) {
+  const int rows = args.rows ? args.rows : args.Hl;
+  if (args.row0 < 0 || rows < 1 || args.row0 + rows > args.Hl) return hipErrorInvalidValue;
   if (mode == 0) {
     // FP16 policy: skip input only (its FP16 hi/lo project operands need twice the feature slice)
-    if (src != BodySrc::Skip || (tile && tile != 16)) return hipErrorInvalidValue;
-    launch_body_t<0, 0, 16>(args, body_fused_num_tiles(0, batch, args.Hl, args.Wl, 16), stream);
+    if (tile == 0) tile = 16;
+    if (src != BodySrc::Skip || (tile != 16 && tile != 8)) return hipErrorInvalidValue;
+    const int tiles = body_fused_num_tiles(0, batch, rows, args.Wl, tile);
+    if (tile == 16) launch_body_t<0, 0, 16>(args, tiles, stream);
+    else launch_body_t<0, 0, 8>(args, tiles, stream);
     return hipGetLastError();
   }
   if (tile == 0) tile = 24;
   if (tile != 24 && (tile != 16 || src == BodySrc::Skip)) return hipErrorInvalidValue;
-  const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl, tile);
+  const int tiles = body_fused_num_tiles(mode, batch, rows, args.Wl, tile);
   switch (mode) {
     case 1: launch_body_m<1>(src, args, tile, tiles, stream); break;
     case 2: launch_body_m<2>(src, args, tile, tiles, stream); break;

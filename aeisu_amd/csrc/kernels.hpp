@@ -53,12 +53,15 @@ struct BodyFusedArgs {
   float analysis[24];      // analysis constants (frame-input variants)
   int Hl, Wl;
   int H, W, py, px;        // frame geometry (frame-input variants)
+  int row0, rows;          // low-grid rows this launch covers: [row0, row0 + rows); rows = 0: all
 };
 // tile = side of the body's output tile in low pixels (0: the policy's default, 24, or 16 for the FP16 policy)
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile = 0);
 // frame-input body: how many leading frames of a batch run on 24x24 tiles (the rest on 16x16 tiles)
 // on a device with `cus` compute units
 int body_fused_split(int mode, int batch, int Hl, int Wl, int cus);
+// FP16 policy (skip input): low rows [0, R) on 16x16 tiles, the rest on 8x8 tiles; returns R
+int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();
 hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
                              hipStream_t stream);
