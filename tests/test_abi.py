@@ -38,6 +38,30 @@ def test_library_exports_every_declared_symbol():
     assert lib.aeisu_version().startswith(b"aeisu_amd")
 
 
+def header_constants():
+    """`#define AEISU_<NAME> <integer>` lines of the public header."""
+    text = (ROOT / "include" / "aeisu_amd.h").read_text()
+    out = {}
+    for name, value in re.findall(r"^#define (AEISU_[A-Z0-9_]+)\s+\(?(-?\d+)u?\)?", text, flags=re.M):
+        out[name] = int(value)
+    return out
+
+
+def test_binding_constants_match_header():
+    """Status codes, precision policies and flags of the ctypes binding are the header's values."""
+    h = header_constants()
+    for name in ("AEISU_ERR_INVALID_ARGUMENT", "AEISU_ERR_ARTIFACT", "AEISU_ERR_HIP", "AEISU_ERR_STATE",
+                 "AEISU_ERR_NONFINITE"):
+        assert getattr(L, name) == h[name], name
+    assert L.PRECISION == {"fp16": h["AEISU_PRECISION_FP16"], "mixed": h["AEISU_PRECISION_MIXED"],
+                           "int8": h["AEISU_PRECISION_INT8"], "mixed-fp8mma": h["AEISU_PRECISION_MIXED_FP8MMA"]}
+    flags = {k[len("AEISU_"):]: v for k, v in h.items() if k.startswith("AEISU_FLAG_")}
+    assert len(flags) >= 5
+    for name, value in flags.items():
+        assert getattr(L, name) == value, name
+    assert len(set(flags.values())) == len(flags) and all(v & (v - 1) == 0 for v in flags.values())
+
+
 def _create(blob: bytes, precision: str):
     h = ctypes.c_void_p()
     buf = ctypes.create_string_buffer(blob, len(blob))
