@@ -9,6 +9,8 @@ specified in words.  This module renders them deterministically:
   of +-0.02, clipped to [0, 1]   (configs 0-3).
 * ``pink_noise``: per-channel 1/f-spectrum colour noise (mean 0.45, std 0.2,
   clipped) rendered at twice the size and 2x bicubic-downsampled (config 4).
+* ``scene_pair`` / ``pink_pair``: the same with the 2x render returned as an
+  HR target for PSNR (scenes are 2x area-downsampled).
 
 All random parameters come from ``numpy.random.default_rng(seed)``; pixel
 arithmetic is float32 torch on the CPU so that frames are identical wherever
@@ -99,8 +101,19 @@ def scene(height: int, width: int, seed: int, shapes: int = 12, texture: bool = 
     return img.clamp(0, 1)
 
 
+def scene_pair(height: int, width: int, seed: int, shapes: int = 12, texture: bool = True):
+    """(LR, HR): the scene rendered at 2x (the HR target) and 2x area-downsampled to height x width."""
+    hr = scene(2 * height, 2 * width, seed, shapes=shapes, texture=texture)
+    return F.avg_pool2d(hr[None], 2)[0], hr
+
+
 def pink_noise(height: int, width: int, seed: int) -> torch.Tensor:
     """3 x height x width 1/f colour noise, rendered at 2x then bicubic-downsampled."""
+    return pink_pair(height, width, seed)[0]
+
+
+def pink_pair(height: int, width: int, seed: int):
+    """(LR, HR) of ``pink_noise``: the 2x render is the HR target."""
     rng = np.random.default_rng(seed)
     hh, ww = 2 * height, 2 * width
     fy = np.fft.fftfreq(hh).reshape(-1, 1)
@@ -116,7 +129,7 @@ def pink_noise(height: int, width: int, seed: int) -> torch.Tensor:
         chans.append(np.clip(0.45 + 0.2 * field, 0.0, 1.0).astype(np.float32))
     hr = torch.from_numpy(np.stack(chans))[None]
     lr = F.interpolate(hr, size=(height, width), mode="bicubic", align_corners=False, antialias=True)
-    return lr[0].clamp(0, 1)
+    return lr[0].clamp(0, 1), hr[0]
 
 
 CONFIGS = {

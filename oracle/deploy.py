@@ -14,28 +14,58 @@ the exact number-format rounding of ``oracle.quant``):
   weight scales and per-tensor activation scales.  Quantization points follow
   optimized/native/src/neural/srcpyr/SrcPyrCudaRuntime.cu:2480-2583 (features
   and project), SrcPyrNativeFp8Compress.cuh:94-129,222-236 (compress),
-  SrcPyrNativeFp8Conv.cuh:459-471,590-596 (bottlenecks),
+  SrcPyrNativeFp8Conv.cuh:459-471,528-606 (bottlenecks),
   SrcPyrNativeFp8Expand.cuh:233-237,280-302 (expand + skip add),
   SrcPyrNativeFp16Refine.cuh:472-475,494-538 (refine + tail),
-  adaptive/AdaptiveReconstruction.cuh:288-417 (head).
+  adaptive/AdaptiveReconstruction.cuh:288-417 (head); scale indices and host
+  reciprocals SrcPyrCudaRuntime.cu:4395-4445, bias selection (``bias_fp8``)
+  SrcPyrCudaRuntime.cu:3814-3817, FP16 tail bias 2999-3006.
 * ``int8`` -- the reference conventional INT8/FP16 policy: symmetric INT8
   activations with ``quantize_s8`` and INT32 accumulation, ``acc*factor+bias``
   epilogues (optimized/shader/src/int8_kernels.cuh:2-62,159-201), expand
-  output ``fp16(q*s_out + skip)`` (int8_kernels.cuh:52-57).  Project, refine
-  and tail use the same FP16/FP32-accumulate arithmetic as ``mixed`` (the
-  reference uses HFMA2 partial sums and a Winograd refine,
-  fusion_kernels.cu:125-190,249-351; this build keeps FP32 accumulation).
+  output ``fp16(q*s_out + skip)`` (int8_kernels.cuh:52-60), scale indices
+  optimized/shader/runtime.py:60-76.  Project, refine and tail use the same
+  FP16/FP32-accumulate arithmetic as ``mixed`` (the reference uses HFMA2
+  partial sums and a Winograd refine, fusion_kernels.cu:125-190,249-351; this
+  build keeps FP32 accumulation).
 
-Parity status: the reference ships no Python for the FP8/INT8 emulations, so
-this file is pinned by (a) the exact E4M3 / INT8 rounding functions (pinned
-in ``oracle.quant``), (b) its FP16 policy agreeing with the FP32 oracle to
-well under 1e-3, and (c) the reference's statistical gates: Mixed-vs-FP16
-output PSNR >= 35 dB (SrcPyrRuntimeTest.cpp:454-457).  Layer-by-layer
-bit-exactness against the reference's CUDA kernels is parity unpinned.
+Accumulation of the E4M3 layers.  The reference runs each of them as a chain
+of ``mma.sync.m16n8k32 ... e4m3.e4m3.f32`` instructions, each adding the sum of
+32 products to the FP32 accumulator (SrcPyrNativeFp8Compress.cuh:166-226,
+SrcPyrNativeFp8Conv.cuh:528-606, SrcPyrNativeFp8Expand.cuh:141-227).  The
+emulation models one instruction as D = fl32(C + exact sum of its 32
+products) (an E4M3 x E4M3 product has at most 8 significant bits and the sums
+stay below 2^26 in multiples of 2^-18, so float64 holds them exactly), applied
+chunk by chunk in the reference's K order:
+
+* compress: 4 chunks; chunk j holds unshuffled channels 32j..32j+31, i.e.
+  skip channels 8j..8j+7 of all four phases (K index c*4 + phase);
+* bottleneck: 9 chunks, one per tap in row-major (dy, dx) order, each the 32
+  input channels of the output channel's group;
+* expand: 2 chunks, input channels 0..31 then 32..63.
+
+INT8 sums are integers (exact in any order).  FP16 layers (project, refine,
+tail) are summed exactly and rounded once; their outputs are FP16-rounded,
+which hides the order of the FP32 sum except in rare one-ulp cases.
+
+Pinning (tests/test_deploy.py): every stage function is checked against a
+brute-force rational-arithmetic restatement of the reference expression on
+inputs built to expose its rounding points (chunked FP32 accumulation,
+``fmaf`` epilogue, FP16 tail bias, contracted expand residual, saturating
+E4M3 / INT8 requantization); every FP8 and INT8 layer is bounded against the
+FP32 checkpoint's layer on the same dequantized input (weight-quantization
+error + bias correction + half an output quantum) and a per-layer scale
+slope of 1 within 0.3 %; ``bias_fp8`` is shown to bring the output closer to
+the FP32 model than ``bias`` on the input class each model was calibrated
+for, and the artifacts' ``bias_fp8 - bias`` equals the exporter's recorded
+correction (DIV2K); planted mistakes (``bias`` for ``bias_fp8``, off-by-one
+activation-scale indices, an unrounded tail bias, a split expand residual,
+float64 or phase-major instead of the reference's chunked FP32 accumulation,
+a double-rounded fmaf) each fail one of those checks.
 """
 from __future__ import annotations
 
-from typing import Dict, Mapping
+from typing import Dict, Mapping, Sequence
 
 import numpy as np
 import torch
@@ -46,6 +76,16 @@ from .quant import e4m3_decode, e4m3_round_t, f16, fmaf, quantize_s8
 
 LAYERS = ("project", "compress", "bottleneck0", "bottleneck1", "bottleneck2",
           "bottleneck3", "expand", "refine", "tail")
+BODY = ("compress", "bottleneck0", "bottleneck1", "bottleneck2", "bottleneck3", "expand")
+
+# Activation-scale indices (input, output) of each quantized layer: compress s1 -> s2
+# (SrcPyrCudaRuntime.cu:4397-4408), bottleneck b s(b+2) -> s(b+3) (4427-4436), expand
+# s6 -> s7 (4587-4601); the INT8 route uses the same table (optimized/shader/runtime.py:60-76).
+# Bias of the E4M3 layers: Fp8Bias() returns the bias-corrected ``bias_fp8`` for the adaptive-filter
+# artifacts (SrcPyrCudaRuntime.cu:3814-3817); project, refine and tail keep ``bias``.
+FP8_BIAS = ".b8"
+SCALE_INDEX = {"compress": (1, 2), "bottleneck0": (2, 3), "bottleneck1": (3, 4),
+               "bottleneck2": (4, 5), "bottleneck3": (5, 6), "expand": (6, 7)}
 
 
 def _analysis_from_vector(v) -> Dict[str, torch.Tensor]:
@@ -75,6 +115,17 @@ def weights_from_folded(state: Mapping[str, torch.Tensor]) -> Dict[str, object]:
     return w
 
 
+def fp32_layers(state: Mapping[str, torch.Tensor]) -> Dict[str, Dict[str, torch.Tensor]]:
+    """FP32 checkpoint weights per deployed layer name (bottleneck i = cat(a_{i+1}, b_{i+1}))."""
+    out = {"compress": ("compress_270",), "expand": ("expand_270",)}
+    layers = {k: {"w": state[v[0] + ".weight"].float(), "b": state[v[0] + ".bias"].float()} for k, v in out.items()}
+    for i in range(4):
+        a, b = f"bottleneck_270_a{i + 1}", f"bottleneck_270_b{i + 1}"
+        layers[f"bottleneck{i}"] = {"w": torch.cat((state[a + ".weight"], state[b + ".weight"])).float(),
+                                    "b": torch.cat((state[a + ".bias"], state[b + ".bias"])).float()}
+    return layers
+
+
 def weights_from_spyr(art) -> Dict[str, object]:
     """Mixed/FP16 deployment weights from an oracle.spyr8f8.read() result."""
     t = art["tensors"]
@@ -93,12 +144,12 @@ def weights_from_spyr(art) -> Dict[str, object]:
 
 
 def weights_from_int8(record) -> Dict[str, object]:
-    """INT8/FP16 weights from the shader_precision_v1 payload (Appendix of the artifact)."""
+    """INT8/FP16 weights from the shader_precision_v1 payload (optimized/shader/runtime.py:34-53)."""
     w: Dict[str, object] = dict(_analysis_from_vector(record["analysis_parameters"].numpy()))
     for layer in ("project", "refine", "tail"):
         w[layer + ".w"] = record["half_weights"][layer].float()
         w[layer + ".b"] = record["half_biases"][layer].float()
-    for layer in ("compress", "bottleneck0", "bottleneck1", "bottleneck2", "bottleneck3", "expand"):
+    for layer in BODY:
         w[layer + ".wq"] = record["int8_weights"][layer].float()
         w[layer + ".factor"] = record["int8_factors"][layer].float()
         w[layer + ".b"] = record["int8_biases"][layer].float()
@@ -107,18 +158,58 @@ def weights_from_int8(record) -> Dict[str, object]:
     return w
 
 
+# ------------------------------------------------------------------------------------------------
+# accumulation
+# ------------------------------------------------------------------------------------------------
 def _conv64(x: torch.Tensor, w: torch.Tensor, groups: int = 1) -> torch.Tensor:
-    """Convolution accumulated in float64 then rounded once to float32."""
+    """Convolution summed exactly (float64) and rounded once to float32 (FP16 layers, INT8 sums)."""
     return F.conv2d(x.double(), w.double(), padding=w.shape[-1] // 2, groups=groups).float()
 
 
+def chunk_sums(x: torch.Tensor, w: torch.Tensor, layer: str) -> Sequence[torch.Tensor]:
+    """Exact float64 partial sums of the K=32 chunks of an E4M3 layer, in the reference's order.
+
+    ``x`` holds E4M3 values [B, Cin, H, W] (for compress: the unshuffled skip, channel c*4+phase),
+    ``w`` E4M3 weight values [Cout, Cin, k, k].
+    """
+    x64, w64 = x.double(), w.double()
+    if layer == "compress" or layer == "expand":
+        return [F.conv2d(x64[:, 32 * j:32 * j + 32], w64[:, 32 * j:32 * j + 32]) for j in range(x.shape[1] // 32)]
+    h, wd = x.shape[-2:]
+    xp = F.pad(x64, (1, 1, 1, 1))
+    return [F.conv2d(xp[:, :, dy:dy + h, dx:dx + wd], w64[:, :, dy:dy + 1, dx:dx + 1], groups=2)
+            for dy in range(3) for dx in range(3)]
+
+
+def mma_chain(parts: Sequence[torch.Tensor]) -> torch.Tensor:
+    """FP32 accumulator over exact chunk sums: acc <- fl32(acc + chunk), acc starting at 0.
+
+    acc is a float32 multiple of 2^-18 and the chunk an exact multiple of 2^-18 below 2^26, so
+    their float64 sum is exact and its rounding to float32 is the single rounding of one MMA.
+    """
+    acc = torch.zeros_like(parts[0], dtype=torch.float32)
+    for part in parts:
+        acc = (acc.double() + part).float()
+    return acc
+
+
+# ------------------------------------------------------------------------------------------------
+# stages
+# ------------------------------------------------------------------------------------------------
 def _chan(v: torch.Tensor) -> torch.Tensor:
     return v.view(1, -1, 1, 1)
 
 
 def _inv(s) -> float:
-    """float32(1) / float32(s): the host-side reciprocal of SrcPyrCudaRuntime.cu:4403."""
+    """float32(1) / float32(s): the host-side reciprocal of SrcPyrCudaRuntime.cu:4403 and
+    optimized/shader/src/int8_kernels.cuh:84,149."""
     return float(np.float32(1.0) / np.float32(s))
+
+
+def _scales(w, layer: str):
+    i, o = SCALE_INDEX[layer]
+    act = w["act"]
+    return float(act[i]), float(act[o])
 
 
 def features(src: torch.Tensor, w: Mapping[str, object]) -> torch.Tensor:
@@ -132,19 +223,87 @@ def project(feat: torch.Tensor, w) -> torch.Tensor:
     return f16(M.leaky(acc))
 
 
-def _fp8_epilogue(acc, w, layer, s_in, s_out) -> torch.Tensor:
-    """fmaf(acc, s_in*wscale, bias_fp8) -> leaky -> e4m3(v * 1/s_out)."""
-    scale = (torch.tensor(float(s_in), dtype=torch.float32) * w[layer + ".ws"].float())
-    v = fmaf(acc, _chan(scale), _chan(w[layer + ".b8"]))
+def fp8_compress_input(skip: torch.Tensor, w) -> torch.Tensor:
+    """E4M3 values of unshuffle(skip) * fl32(1/s1) (SrcPyrNativeFp8Compress.cuh:94-129)."""
+    s_in, _ = _scales(w, "compress")
+    return e4m3_round_t(F.pixel_unshuffle(skip, 2) * torch.tensor(_inv(s_in), dtype=torch.float32))
+
+
+def fp8_pre_round(acc, w, layer: str):
+    """The float32 value an E4M3 layer's epilogue rounds, and the magnitude of the terms it came
+    from (|acc * scale| + |bias|, times 1/s_out: the scale of its accumulated rounding differences)."""
+    s_in, s_out = _scales(w, layer)
+    scale = torch.tensor(s_in, dtype=torch.float32) * w[layer + ".ws"].float()
+    bias = w[layer + FP8_BIAS].float()
+    v = fmaf(acc, _chan(scale), _chan(bias))
     v = torch.where(v < 0, v * _chan(w[layer + ".prelu"]), v)
-    return e4m3_round_t(v * torch.tensor(_inv(s_out), dtype=torch.float32))
+    inv = torch.tensor(_inv(s_out), dtype=torch.float32)
+    return v * inv, ((acc * _chan(scale)).abs() + _chan(bias).abs()) * inv
 
 
-def _int8_epilogue(acc, w, layer, s_out) -> torch.Tensor:
-    """fmaf(acc, factor, bias) -> leaky(0.1) -> quantize_s8(v, 1/s_out) (integer-valued float)."""
+def fp8_epilogue(acc, w, layer: str) -> torch.Tensor:
+    """fmaf(acc, fl32(s_in * wscale), bias_fp8) -> LeakyReLU -> e4m3(v * fl32(1/s_out)).
+
+    SrcPyrNativeFp8Compress.cuh:145-163,229-236 (and the same lines of the grouped and expand kernels).
+    """
+    return e4m3_round_t(fp8_pre_round(acc, w, layer)[0])
+
+
+def fp8_acc(x: torch.Tensor, w, layer: str) -> torch.Tensor:
+    """FP32 accumulator of an E4M3 layer on E4M3 values ``x``."""
+    return mma_chain(chunk_sums(x, w[layer + ".w8"], layer))
+
+
+def fp8_layer(x: torch.Tensor, w, layer: str) -> torch.Tensor:
+    """One E4M3 layer: E4M3 values in, E4M3 values out."""
+    return fp8_epilogue(fp8_acc(x, w, layer), w, layer)
+
+
+def expand_residual(q: torch.Tensor, s7: float, skip: torch.Tensor) -> torch.Tensor:
+    """fp16(fmaf(pixel_shuffle(q), s7, skip)): ``float(q) * s7 + skip`` contracted into one FMA by
+    nvcc -O3 (SrcPyrNativeFp8Expand.cuh:290-302; int8_kernels.cuh:60 under --use_fast_math)."""
+    return f16(fmaf(F.pixel_shuffle(q, 2), float(np.float32(s7)), skip))
+
+
+def int8_input(skip: torch.Tensor, w) -> torch.Tensor:
+    """quantize_s8(unshuffle(skip), 1/s1) (int8_kernels.cuh:24-29)."""
+    s_in, _ = _scales(w, "compress")
+    return quantize_s8(F.pixel_unshuffle(skip, 2), _inv(s_in))
+
+
+def int8_pre_round(acc, w, layer: str):
+    """The float32 value an INT8 layer's epilogue rounds to an integer, and its terms' magnitude."""
+    _, s_out = _scales(w, layer)
     v = fmaf(acc, _chan(w[layer + ".factor"]), _chan(w[layer + ".b"]))
     v = torch.where(v >= 0, v, v * torch.tensor(0.1, dtype=torch.float32))
-    return quantize_s8(v, _inv(s_out))
+    inv = torch.tensor(_inv(s_out), dtype=torch.float32)
+    return v * inv, ((acc * _chan(w[layer + ".factor"])).abs() + _chan(w[layer + ".b"]).abs()) * inv
+
+
+def int8_epilogue(acc, w, layer: str) -> torch.Tensor:
+    """fmaf(acc, factor, bias) -> leaky(0.1) -> quantize_s8(v, 1/s_out) (int8_kernels.cuh:47-50)."""
+    t = int8_pre_round(acc, w, layer)[0]
+    return torch.clamp(torch.round(t), -127, 127)
+
+
+def int8_acc(x: torch.Tensor, w, layer: str) -> torch.Tensor:
+    """INT32 accumulator (exact, as float32: |acc| <= 127 * 127 * 288 < 2^24) of an INT8 layer."""
+    return _conv64(x, w[layer + ".wq"], 2 if layer.startswith("bottleneck") else 1)
+
+
+def int8_layer(x: torch.Tensor, w, layer: str) -> torch.Tensor:
+    return int8_epilogue(int8_acc(x, w, layer), w, layer)
+
+
+def refine(work: torch.Tensor, w) -> torch.Tensor:
+    """fp16(leaky(W16 * work + bias)) with the FP32 ``.bias`` (SrcPyrNativeFp16Refine.cuh:472-475)."""
+    return f16(M.leaky(_conv64(work, w["refine.w"]) + _chan(w["refine.b"])))
+
+
+def tail(dec: torch.Tensor, w) -> torch.Tensor:
+    """fp16(W16 . dec + fp16(bias)) (SrcPyrNativeFp16Refine.cuh:494-538; bias rounded on the host,
+    SrcPyrCudaRuntime.cu:2999-3006)."""
+    return f16(_conv64(dec, w["tail.w"]) + _chan(f16(w["tail.b"])))
 
 
 def controller(src: torch.Tensor, w: Mapping[str, object], precision: str,
@@ -152,7 +311,9 @@ def controller(src: torch.Tensor, w: Mapping[str, object], precision: str,
     """Packed FP16 coefficients [B,64,Hp/2,Wp/2] under the given precision policy.
 
     ``src`` is the padded source (values already FP16-representable for the
-    GPU configs).  ``record`` (optional) receives the intermediate tensors.
+    GPU configs).  ``record`` (optional) receives the intermediate tensors:
+    features, skip, low0..low4 (E4M3 values / INT8 codes / FP16 values),
+    work, refine, meta.
     """
     rec = record if record is not None else {}
     if precision == "fp16":
@@ -165,7 +326,6 @@ def controller(src: torch.Tensor, w: Mapping[str, object], precision: str,
         feat = features(src, w)
         skip = project(feat, w)
     rec["features"], rec["skip"] = feat, skip
-    act = w.get("act")
     if precision == "fp16":
         low = f16(M.leaky(_conv64(F.pixel_unshuffle(skip, 2), w["compress.w"]) + _chan(w["compress.b"])))
         rec["low0"] = low
@@ -174,32 +334,23 @@ def controller(src: torch.Tensor, w: Mapping[str, object], precision: str,
             rec[f"low{i + 1}"] = low
         e = f16(M.leaky(_conv64(low, w["expand.w"]) + _chan(w["expand.b"])))
         work = f16(F.pixel_shuffle(e, 2) + skip)
-    elif precision == "mixed":
-        x = e4m3_round_t(F.pixel_unshuffle(skip, 2) * torch.tensor(_inv(act[1]), dtype=torch.float32))
-        low = _fp8_epilogue(_conv64(x, w["compress.w8"]), w, "compress", act[1], act[2])
+    elif precision in ("mixed", "int8"):
+        layer_fn, x = (fp8_layer, fp8_compress_input(skip, w)) if precision == "mixed" else (int8_layer, int8_input(skip, w))
+        rec["compress_in"] = x
+        low = layer_fn(x, w, "compress")
         rec["low0"] = low
         for i in range(4):
-            acc = _conv64(low, w[f"bottleneck{i}.w8"], groups=2)
-            low = _fp8_epilogue(acc, w, f"bottleneck{i}", act[i + 2], act[i + 3])
+            low = layer_fn(low, w, f"bottleneck{i}")
             rec[f"low{i + 1}"] = low
-        q = _fp8_epilogue(_conv64(low, w["expand.w8"]), w, "expand", act[6], act[7])
-        work = f16(fmaf(F.pixel_shuffle(q, 2), float(act[7]), skip))
-    elif precision == "int8":
-        x = quantize_s8(F.pixel_unshuffle(skip, 2), _inv(act[1]))
-        low = _int8_epilogue(_conv64(x, w["compress.wq"]), w, "compress", act[2])
-        rec["low0"] = low
-        for i in range(4):
-            acc = _conv64(low, w[f"bottleneck{i}.wq"], groups=2)
-            low = _int8_epilogue(acc, w, f"bottleneck{i}", act[i + 3])
-            rec[f"low{i + 1}"] = low
-        q = _int8_epilogue(_conv64(low, w["expand.wq"]), w, "expand", act[7])
-        work = f16(fmaf(F.pixel_shuffle(q, 2), float(act[7]), skip))
+        q = layer_fn(low, w, "expand")
+        rec["expand_out"] = q
+        work = expand_residual(q, _scales(w, "expand")[1], skip)
     else:
         raise ValueError(f"unknown precision {precision!r}")
     rec["work"] = work
-    dec = f16(M.leaky(_conv64(work, w["refine.w"]) + _chan(w["refine.b"])))
+    dec = refine(work, w)
     rec["refine"] = dec
-    meta = f16(_conv64(dec, w["tail.w"]) + _chan(f16(w["tail.b"])))
+    meta = tail(dec, w)
     rec["meta"] = meta
     return meta
 

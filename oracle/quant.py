@@ -17,6 +17,8 @@ the even code), and both against ``torch.float8_e4m3fn`` for in-range values.
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 
@@ -48,6 +50,31 @@ def e4m3_decode(codes) -> np.ndarray:
 
 def e4m3_round(x) -> np.ndarray:
     """Round float32 values to the nearest E4M3 value (RNE, saturating). Returns float32."""
+    return e4m3_round_t(torch.from_numpy(np.ascontiguousarray(np.asarray(x, dtype=np.float32)))).numpy()
+
+
+def e4m3_round_t(x: torch.Tensor) -> torch.Tensor:
+    """Round float32 values to the nearest E4M3 value (RNE, saturating), on float32 bit patterns.
+
+    Normal E4M3 range (|x| >= 2^-6): keep 3 of the 23 mantissa bits, round half to even on the
+    bit pattern (a carry out of the mantissa steps the exponent, as RNE requires).  Below 2^-6 the
+    quantum is fixed at 2^-9: x * 2^9 is exact, torch.round is half to even.  Then saturate to
+    +-448 (values from 464 up would round to the NaN code 0x7F).
+    """
+    x = x.detach().to(torch.float32).cpu()
+    x = torch.clamp(x, -1024.0, 1024.0).contiguous()    # keeps the bit arithmetic below float32 max
+    bits = x.view(torch.int32)
+    bias = ((bits >> 20) & 1) + 0x7FFFF
+    normal = ((bits + bias) & ~0xFFFFF).view(torch.float32)
+    sub = torch.round(x * 512.0) / 512.0
+    out = torch.where(x.abs() < 2.0 ** -6, sub, normal)
+    out = torch.clamp(out, -E4M3_MAX, E4M3_MAX)
+    return torch.where(torch.isnan(x), x, out)
+
+
+def e4m3_round_by_quantum(x) -> np.ndarray:
+    """Second, independent formulation of e4m3_round (binade quantum from log2, float64), used
+    to cross-check the bit-pattern version."""
     v = np.asarray(x, dtype=np.float32).astype(np.float64)
     mag = np.abs(v)
     # exponent of the binade, floor(log2|v|), subnormal range pinned at -6
@@ -73,11 +100,6 @@ def e4m3_encode(x) -> np.ndarray:
     return np.where(np.isnan(r), np.uint8(0x7F), codes).astype(np.uint8)
 
 
-def e4m3_round_t(x: torch.Tensor) -> torch.Tensor:
-    """Torch wrapper of e4m3_round (CPU)."""
-    return torch.from_numpy(e4m3_round(x.detach().cpu().numpy().astype(np.float32)))
-
-
 def f16(x: torch.Tensor) -> torch.Tensor:
     """Round to FP16 (RNE) and return float32."""
     return x.to(torch.float16).to(torch.float32)
@@ -89,9 +111,46 @@ def quantize_s8(v: torch.Tensor, inv_scale: float) -> torch.Tensor:
     return torch.clamp(torch.round(prod), -127, 127)   # torch.round: half to even
 
 
+def round_f32(s: torch.Tensor, err: torch.Tensor) -> torch.Tensor:
+    """float32 RNE of the exact value s + err, where s is float64 and |err| <= ulp64(s)/2.
+
+    Rounding s alone is right unless s sits exactly on a float32 midpoint and
+    err breaks the tie (the float64 sum already rounded once); then the exact
+    value lies on err's side of the midpoint.
+    """
+    r = s.to(torch.float32)
+    r64 = r.to(torch.float64)
+    up = torch.nextafter(r, torch.full_like(r, math.inf))
+    dn = torch.nextafter(r, torch.full_like(r, -math.inf))
+    at_up_mid = s == (r64 + up.to(torch.float64)) / 2
+    at_dn_mid = s == (r64 + dn.to(torch.float64)) / 2
+    r = torch.where(at_up_mid & (err > 0), up, r)
+    return torch.where(at_dn_mid & (err < 0), dn, r)
+
+
 def fmaf(a: torch.Tensor, b, c) -> torch.Tensor:
-    """float32 fused multiply-add emulated in float64 (one rounding to float32)."""
-    a64 = a.to(torch.float64)
+    """float32 fused multiply-add a*b + c with one rounding (C fmaf / v_fma_f32).
+
+    a*b of two float32 values is exact in float64 (48 significant bits); the
+    float64 sum with c is split into its rounded value and exact error
+    (Knuth's TwoSum) so that the final float32 rounding is the correct one.
+    """
+    a64 = torch.as_tensor(a, dtype=torch.float32).to(torch.float64)
     b64 = torch.as_tensor(b, dtype=torch.float32).to(torch.float64)
     c64 = torch.as_tensor(c, dtype=torch.float32).to(torch.float64)
-    return (a64 * b64 + c64).to(torch.float32)
+    p = a64 * b64
+    c64 = c64.expand_as(p)
+    s = p + c64
+    r = s.to(torch.float32)
+    # Only a float64 sum lying exactly on a float32 midpoint can round the wrong way: its low
+    # 29 mantissa bits are 1 followed by 28 zeros (float32-normal range; smaller values take the
+    # general path too).
+    mid = (s.contiguous().view(torch.int64) & 0x1FFFFFFF) == 0x10000000
+    mid |= (s != 0) & (s.abs() < 2.0 ** -125)
+    if bool(mid.any()):
+        sm, pm, cm = s[mid], p[mid], c64[mid]
+        bb = sm - pm
+        err = (pm - (sm - bb)) + (cm - bb)
+        r = r.clone()
+        r[mid] = round_f32(sm, err)
+    return r

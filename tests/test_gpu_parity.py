@@ -1,11 +1,15 @@
 """GPU parity of the HIP runtime against the CPU oracle and the reference's golden vectors.
 
 Tolerances:
-* FP16 policy vs the reference FP32 model: <= 1e-3 max-abs on [0,1] RGB.
+* FP16 policy vs the reference FP32 model: <= 1e-3 max-abs on [0,1] RGB
+  (white-noise goldens: 3e-3, the FP16 storage bound; see that test).
 * Mixed FP8 / INT8 policies vs their CPU emulation: <= 2/255 max-abs and
   output PSNR within 0.05 dB against a target.
 * Phase packing / indexing: exact (checked through the head on synthetic
   coefficients and through tile-vs-whole agreement).
+
+Layer-by-layer parity is in test_gpu_layers.py, full-size configurations in
+test_gpu_fullsize.py.
 """
 from __future__ import annotations
 
@@ -18,7 +22,7 @@ import torch
 from oracle import deploy as D
 from oracle import model as M
 from oracle import spyr8f8
-from tests._util import WEIGHTS, crop_output, golden, nhwc_to_nchw, pad_frame, psnr, y_psnr
+from tests._util import WEIGHTS, crop_output, golden, pad_frame, psnr, y_psnr
 
 pytestmark = pytest.mark.gpu
 
@@ -132,18 +136,6 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
 # ------------------------------------------------------------------------------------------------
 # controller and end-to-end, FP16 policy
 # ------------------------------------------------------------------------------------------------
-def test_controller_fp16_matches_emulation(fp16_model, area_state):
-    say("case: FP16 controller vs oracle fp16 emulation (80x120)")
-    src = _frame(80, 120, 7)
-    padded = pad_frame(src[None])
-    rec = {}
-    meta_ref = D.controller(padded, D.weights_from_folded(area_state), "fp16", rec)
-    got = nhwc_to_nchw(fp16_model.controller(src[None].cuda().contiguous()).float().cpu())
-    err = (got - meta_ref).abs()
-    say(f"  meta max {err.max().item():.3g} mean {err.mean().item():.3g}")
-    assert err.max().item() < 0.05 and err.mean().item() < 2e-3
-
-
 @pytest.mark.parametrize("case", ["small", "tiling"])
 def test_fp16_end_to_end_vs_reference_golden(fp16_model, area_state, R, case):
     """Uniform-noise golden frames: the worst case for FP16 activation storage.
@@ -328,8 +320,9 @@ def test_mixed_matches_emulation(mixed_model, area_state):
 
 
 def test_mixed_fp8_mfma_variant(R, area_state):
-    """E4M3 operands on the FP8 MFMA: the unit rounds inside its accumulation (~1e-5 relative),
-    so rare requantization flips are expected; held to PSNR >= 60 dB and 4/255 vs the emulation."""
+    """E4M3 operands on the FP8 MFMA (AEISU_PRECISION_MIXED_FP8MMA, not a deliverable policy): the unit
+    rounds inside its accumulation (~1e-5 relative), so about 1e-3 of each layer's codes flip
+    (test_gpu_layers.py) and isolated outputs move by up to ~3/255; held to PSNR >= 60 dB and 4/255."""
     say("case: Mixed on the FP8 MFMA vs emulation (96x160)")
     model = R.load_model(WEIGHTS / "aeisu_area_mixed_fp8.bin", precision="mixed-fp8mma")
     w = D.weights_from_spyr(spyr8f8.read_file(WEIGHTS / "aeisu_area_mixed_fp8.bin"))
@@ -350,14 +343,9 @@ def test_int8_matches_emulation(int8_model):
 
 
 def test_mixed_psnr_delta_vs_target(mixed_model):
-    """Config-4 style frame with a matched HR target: GPU and emulation Y-PSNR agree within 0.05 dB.
-
-    1/f noise drives ~10^7 E4M3 requantizations per frame; the GPU sums in FP32
-    and the emulation in FP64, so a handful of values that sit within an FP32
-    ulp of an E4M3 rounding midpoint flip by one code.  Isolated output pixels
-    then move by slightly more than 2/255 (2.2/255 observed), so this stress
-    frame is held to 3/255 max-abs; scene frames stay at 2/255.
-    """
+    """Config-4 style frame with a matched HR target: GPU and emulation Y-PSNR agree within 0.05 dB
+    and the outputs within 2/255 (the full-size tests count the rare values an FP16-layer rounding
+    flip moves further)."""
     from aeisu_amd import frames
     say("case: Mixed Y-PSNR delta vs HR target (1/f noise, 144x256)")
     hr = frames.pink_noise(288, 512, 4)
@@ -369,4 +357,4 @@ def test_mixed_psnr_delta_vs_target(mixed_model):
     d = y_psnr(got, hr) - y_psnr(ref, hr)
     say(f"  Y-PSNR gpu {y_psnr(got, hr):.4f} emu {y_psnr(ref, hr):.4f} delta {d:.4f} dB")
     assert abs(d) <= 0.05
-    assert (got - ref).abs().max().item() <= 3 / 255
+    assert (got - ref).abs().max().item() <= 2 / 255
