@@ -29,7 +29,10 @@ _P, _I, _U, _S = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint, ctypes.c_size_t
 SIGNATURES = {
     "aeisu_create_from_file": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
     "aeisu_create_from_memory": (_I, [_P, _S, _I, ctypes.POINTER(_P)]),
-    "aeisu_configure": (_I, [_P, _I, _I, _I, _I, _I, _U]),
+    "aeisu_create_sibling": (_I, [_P, ctypes.POINTER(_P)]),
+    "aeisu_shares_weights": (_I, [_P, _P]),
+    "aeisu_configure": (_I, [_P, _I, _I, _I, _I, _I, _I, _U]),
+    "aeisu_startup_report": (_S, [_P, ctypes.c_char_p, _S]),
     "aeisu_upscale_async": (_I, [_P, _P, _P, _P]),
     "aeisu_upscale": (_I, [_P, _P, _P, _P]),
     "aeisu_upscale_graph": (_I, [_P, _P, _P, _P]),

@@ -37,8 +37,22 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+ABI_SMOKE_SRC = ROOT / "tests" / "abi_smoke.cpp"
+ABI_SMOKE = ROOT / "tests" / "abi_smoke"
+
+
+def build_abi_smoke() -> Path:
+    """The C++ program that exercises the public header against the built library (a GPU test runs it)."""
+    cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", f"-I{ROOT / 'include'}", str(ABI_SMOKE_SRC),
+           "-o", str(ABI_SMOKE), f"-L{PKG}", "-laeisu_amd", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN/../aeisu_amd"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"abi_smoke build failed:\n{res.stderr}")
+    return ABI_SMOKE
+
+
 def build(jobs: int = 8) -> Path:
-    """Compile every source (always) and link the shared library."""
+    """Compile every source (always), link the shared library and the C++ ABI test program."""
     BUILD.mkdir(exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, sources()))
@@ -48,6 +62,7 @@ def build(jobs: int = 8) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_abi_smoke()
     return LIB
 
 

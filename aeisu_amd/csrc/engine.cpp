@@ -13,6 +13,8 @@
 #include <fstream>
 #include <functional>
 #include <memory>
+#include <mutex>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -259,34 +261,117 @@ struct LayerDev {
 // ------------------------------------------------------------------------------------------------
 constexpr int kStageEvents = AEISU_STAGE_COUNT;  // 7 boundaries per frame (start + 6 stage ends)
 constexpr int kMaxTimedFrames = 4096;
+constexpr int kModes = 4;
 
-struct Runtime {
-  int device = 0, precision = 0, mode = 0, cu_count = 0;
+// Kernel mode of a precision: 0 FP16, 1 E4M3 on the FP8 MFMA, 2 INT8, 3 E4M3 values on the FP16 MFMA.
+static int mode_of(int precision) {
+  switch (precision) {
+    case AEISU_PRECISION_FP16: return 0;
+    case AEISU_PRECISION_MIXED_FP8MMA: return 1;
+    case AEISU_PRECISION_INT8: return 2;
+    case AEISU_PRECISION_MIXED: return 3;
+    default: fail(AEISU_ERR_INVALID_ARGUMENT, "unknown precision");
+  }
+}
+static const char* precision_name(int mode) {
+  static const char* names[kModes] = {"FP16", "FP8-E4M3 on the FP8 MFMA", "INT8/FP16", "FP8/FP16-Mixed"};
+  return names[mode];
+}
+
+// Weights of one arithmetic policy, packed into MFMA fragments and resident on the device.
+struct ModeWeights {
+  int mode = 0;
   bool project_precise = false;
-  std::string checksum;
   float analysis[24];
   float act[10] = {};
   LayerDev project, compress, grouped[4], expand, refine_tail, head;
   DeviceBuffer compress_rgb;       // INT8 compress weights in the frame-input fused body's K order
   DeviceBuffer tail_bias;
   DeviceBuffer body_consts;        // epilogue constants of the fused body (kBodyConsts floats)
-  // geometry
-  bool configured = false;
+
+  // every device buffer, for commit() and byte accounting
+  template <typename Fn>
+  void each_buffer(Fn fn) {
+    for (LayerDev* l : {&project, &compress, &grouped[0], &grouped[1], &grouped[2], &grouped[3], &expand,
+                        &refine_tail, &head}) {
+      fn(l->frag);
+      fn(l->bias);
+      fn(l->scale);
+    }
+    fn(compress_rgb);
+    fn(tail_bias);
+    fn(body_consts);
+  }
+  size_t bytes() const {
+    size_t n = 0;
+    const_cast<ModeWeights*>(this)->each_buffer([&](DeviceBuffer& b) { n += b.bytes; });
+    return n;
+  }
+};
+
+// The loaded artifact and its uploaded weights: shared by a runtime and its siblings (the reference's
+// shared execution engine, SrcPyrCudaRuntime.cu:5392-5396).  A policy's weights are packed and uploaded
+// the first time a runtime is configured for it.
+struct Model {
+  Artifact art;
+  int device = 0, cu_count = 0;
+  std::string gpu_name, gcn_arch;
+  int hip_runtime_version = 0;
+  std::mutex mu;
+  std::unique_ptr<ModeWeights> modes[kModes];
+
+  const ModeWeights& weights(int mode);
+  size_t bytes() {
+    std::lock_guard<std::mutex> lock(mu);
+    size_t n = 0;
+    for (const auto& m : modes)
+      if (m) n += m->bytes();
+    return n;
+  }
+};
+
+// Frame geometry and launch shapes of one configuration: a pure function of the policy, the device's
+// CU count and the configure arguments (computed without allocating).
+struct Geometry {
   int batch = 0, H = 0, W = 0, Hp = 0, Wp = 0, py = 0, px = 0, Hq = 0, Wq = 0, Hl = 0, Wl = 0;
   int in_fp32 = 0, out_fp32 = 0;
   unsigned flags = 0;
-  DeviceBuffer skip, work, meta, nonfinite;
-  DeviceBuffer low[5];
-  int nlow = 2;
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
-  int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
-  int body_rows16 = 0;             // FP16 policy body: low rows on 16x16 tiles, the rest on 8x8
   bool fused_rgb = false;          // the fused body takes the frames (project recomputed on chip,
                                    // no skip tensor); the quantized policies
-  bool fused_ready = false;        // fused kernels' LDS limit raised on this device
+  int nlow = 0;                    // body activations in device memory (per-layer path)
+  int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
+  int body_rows16 = 0;             // FP16 policy body: low rows on 16x16 tiles, the rest on 8x8
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
-  // captured frame graphs, one per (input, output) buffer pair (a small LRU-free cache)
+
+  size_t packed() const { return size_t(batch) * Hq * Wq; }
+  size_t lowpx() const { return size_t(batch) * Hl * Wl; }
+  // device scratch of the configuration (bytes): skip, work, meta, low activations
+  size_t skip_bytes() const { return fused_rgb ? 0 : packed() * 32 * 2; }
+  size_t work_bytes() const { return packed() * 32 * 2; }
+  size_t meta_bytes() const { return fused ? 0 : packed() * 64 * 2; }
+};
+
+// Device pointers the kernels of one frame use beyond the inputs, outputs and weights.
+struct Scratch {
+  void* skip = nullptr;
+  void* work = nullptr;
+  void* meta = nullptr;
+  void* low[5] = {};
+  unsigned* nonfinite = nullptr;
+};
+
+struct Runtime {
+  std::shared_ptr<Model> model;
+  int precision = 0, mode = 0;
+  const ModeWeights* w = nullptr;  // the policy this runtime runs
+  bool configured = false;
+  Geometry g;
+  DeviceBuffer skip, work, meta, nonfinite;
+  DeviceBuffer low[5];
+  std::string report;              // startup report of the configuration
+  // captured frame graphs, one per (input, output) buffer pair
   struct Graph {
     const void* in;
     void* out;
@@ -301,20 +386,32 @@ struct Runtime {
   int timed_frames = 0;
 
   ~Runtime() {
-    (void)hipSetDevice(device);
+    if (model) (void)hipSetDevice(model->device);
     drop_graph();
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
   }
   void drop_graph() {
-    for (Graph& g : graphs) {
-      (void)hipGraphExecDestroy(g.exec);
-      (void)hipGraphDestroy(g.graph);
+    for (Graph& gr : graphs) {
+      (void)hipGraphExecDestroy(gr.exec);
+      (void)hipGraphDestroy(gr.graph);
     }
     graphs.clear();
   }
-
-  size_t low_elem() const { return mode == 0 ? 2 : 1; }
+  Scratch scratch() {
+    Scratch sc;
+    sc.skip = skip.ptr;
+    sc.work = work.ptr;
+    sc.meta = meta.ptr;
+    for (int i = 0; i < 5; ++i) sc.low[i] = low[i].ptr;
+    sc.nonfinite = nonfinite.as<unsigned>();
+    return sc;
+  }
+  size_t scratch_bytes() const {
+    size_t n = skip.bytes + work.bytes + meta.bytes + nonfinite.bytes;
+    for (const auto& l : low) n += l.bytes;
+    return n;
+  }
 };
 
 static void require_prelu(const Artifact& a, const std::string& layer, uint32_t cout, float value) {
@@ -327,7 +424,7 @@ static void require_prelu(const Artifact& a, const std::string& layer, uint32_t 
 
 static std::vector<float> as_f32_vector(const TensorView& t) { return std::vector<float>(t.f32(), t.f32() + t.count()); }
 
-static void upload_weights(Runtime& rt, const Artifact& a) {
+static void pack_weights(ModeWeights& rt, const Artifact& a) {
   // --- shared tensors and contracts (SrcPyrModel.cpp:355-422)
   const TensorView& stencil = a.need("analysis_stencil", kF32, {24});
   for (int i = 0; i < 24; ++i) {
@@ -561,16 +658,33 @@ static void upload_weights(Runtime& rt, const Artifact& a) {
   }
 }
 
-static void commit_weights(Runtime& rt) {
-  for (LayerDev* l : {&rt.project, &rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3],
-                      &rt.expand, &rt.refine_tail, &rt.head}) {
-    l->frag.commit();
-    l->bias.commit();
-    l->scale.commit();
+static void commit_weights(ModeWeights& w) {
+  w.each_buffer([](DeviceBuffer& b) { b.commit(); });
+}
+
+// Per-device set-up that every launch path needs: the fused kernels' LDS limits.
+static std::mutex g_prepare_mu;
+static bool g_prepared[64];
+static void prepare_device(int device) {
+  std::lock_guard<std::mutex> lock(g_prepare_mu);
+  if (device < 0 || device >= 64) fail(AEISU_ERR_HIP, "device ordinal out of range");
+  if (g_prepared[device]) return;
+  check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
+  check_hip(body_fused_prepare(), "hipFuncSetAttribute(fused body LDS)");
+  g_prepared[device] = true;
+}
+
+const ModeWeights& Model::weights(int mode) {
+  std::lock_guard<std::mutex> lock(mu);
+  if (!modes[mode]) {
+    auto w = std::make_unique<ModeWeights>();
+    w->mode = mode;
+    pack_weights(*w, art);          // host-only: validates every tensor the policy needs
+    check_hip(hipSetDevice(device), "hipSetDevice");
+    commit_weights(*w);
+    modes[mode] = std::move(w);
   }
-  rt.compress_rgb.commit();
-  rt.tail_bias.commit();
-  rt.body_consts.commit();
+  return *modes[mode];
 }
 
 static int clamp_grid(int tiles, int per_cu, int cus) {
@@ -579,7 +693,8 @@ static int clamp_grid(int tiles, int per_cu, int cus) {
   return std::max(g, 1);
 }
 
-static void configure(Runtime& rt, int batch, int height, int width, int in_layout, int out_layout, unsigned flags) {
+static Geometry make_geometry(int mode, bool project_precise, int cus, int batch, int height, int width, int in_layout,
+                              int out_layout, unsigned flags) {
   if (batch <= 0 || height <= 0 || width <= 0) fail(AEISU_ERR_INVALID_ARGUMENT, "batch, height and width must be positive");
   if (height > 8192 || width > 8192 || batch > 1024) fail(AEISU_ERR_INVALID_ARGUMENT, "frame dimensions exceed 8192 (or batch > 1024)");
   if ((in_layout != AEISU_LAYOUT_NCHW_F16 && in_layout != AEISU_LAYOUT_NCHW_F32) ||
@@ -591,181 +706,221 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   const bool no_pad = flags & AEISU_FLAG_NO_PAD;
   if (no_pad && (height % 4 || width % 4))
     fail(AEISU_ERR_INVALID_ARGUMENT, "Source H/W must be divisible by 4");
-  rt.drop_graph();
-  rt.configured = false;
-  rt.timed_frames = 0;                 // recorded stage events belong to the previous layout
-  rt.batch = batch;
-  rt.H = height;
-  rt.W = width;
+  Geometry g;
+  g.batch = batch;
+  g.H = height;
+  g.W = width;
   if (no_pad) {
     // The caller passes a frame that is already on the padded grid (aeisu/model.py:473-479).
-    rt.py = rt.px = 0;
-    rt.Hp = height;
-    rt.Wp = width;
+    g.py = g.px = 0;
+    g.Hp = height;
+    g.Wp = width;
   } else {
     // align32 + halo16 replicate padding (aeisu/runtime.py:82-84), realised by clamped reads.
     const int ey = (32 - height % 32) % 32, ex = (32 - width % 32) % 32;
-    rt.py = 16 + ey / 2;
-    rt.px = 16 + ex / 2;
-    rt.Hp = height + 32 + ey;
-    rt.Wp = width + 32 + ex;
+    g.py = 16 + ey / 2;
+    g.px = 16 + ex / 2;
+    g.Hp = height + 32 + ey;
+    g.Wp = width + 32 + ex;
   }
-  rt.Hq = rt.Hp / 2;
-  rt.Wq = rt.Wp / 2;
-  rt.Hl = rt.Hp / 4;
-  rt.Wl = rt.Wp / 4;
-  rt.in_fp32 = in_layout == AEISU_LAYOUT_NCHW_F32;
-  rt.out_fp32 = out_layout == AEISU_LAYOUT_NCHW_F32;
-  rt.flags = flags;
-  const size_t packed = size_t(batch) * rt.Hq * rt.Wq, lowpx = size_t(batch) * rt.Hl * rt.Wl;
-  const bool fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
+  g.Hq = g.Hp / 2;
+  g.Wq = g.Wp / 2;
+  g.Hl = g.Hp / 4;
+  g.Wl = g.Wp / 4;
+  g.in_fp32 = in_layout == AEISU_LAYOUT_NCHW_F32;
+  g.out_fp32 = out_layout == AEISU_LAYOUT_NCHW_F32;
+  g.flags = flags;
+  g.fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
   // the skip tensor only exists in device memory where the project kernel runs
-  const bool fused_rgb = fused && rt.mode != 0;
-  if (fused_rgb) rt.skip.release();
-  else rt.skip.alloc(packed * 32 * 2);
-  rt.work.alloc(packed * 32 * 2);
-  // the coefficient tensor only exists in device memory on the unfused path
-  if (flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED)) rt.meta.alloc(packed * 64 * 2);
-  else rt.meta.release();
+  g.fused_rgb = g.fused && mode != 0;
   // low-resolution activations only reach device memory on the per-layer path
-  rt.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : (fused ? 0 : 2);
-  for (int i = 0; i < 5; ++i) {
-    if (i < rt.nlow) rt.low[i].alloc(lowpx * 64 * rt.low_elem());
-    else rt.low[i].release();
-  }
-  rt.nonfinite.alloc(4);
-  check_hip(hipMemset(rt.nonfinite.ptr, 0, 4), "hipMemset(flag)");
-  const int m = rt.mode, cus = rt.cu_count;
-  const int low_groups = batch * rt.Hl * ((rt.Wl + 15) / 16);
-  rt.grid.project = clamp_grid(project_num_tiles(batch, rt.Hq, rt.Wq), project_blocks_per_cu(rt.in_fp32, rt.project_precise), cus);
-  rt.grid.compress = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(0, m), cus);
-  rt.grid.grouped = clamp_grid(grouped_num_tiles(batch, rt.Hl, rt.Wl), body_blocks_per_cu(1, m), cus);
-  rt.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, m), cus);
-  rt.grid.refine = clamp_grid(refine_num_tiles(batch, rt.Hq, rt.Wq), refine_blocks_per_cu(), cus);
-  rt.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(rt.in_fp32, rt.out_fp32), cus);
-  rt.fused = fused;
-  rt.fused_rgb = fused_rgb;
-  rt.body_split = (flags & AEISU_FLAG_BODY_TILE24) ? batch : body_fused_split(m, batch, rt.Hl, rt.Wl, cus);
-  rt.body_rows16 = (flags & AEISU_FLAG_BODY_TILE24) ? rt.Hl : body_fused_row_split(m, batch, rt.Hl, rt.Wl, cus);
-  rt.grid.fused = clamp_grid(fused_num_tiles(rt.in_fp32, batch, height, width, rt.Hq, rt.Wq, rt.py, rt.px), 1, cus);
-  if (rt.fused && !rt.fused_ready) {
-    check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
-    check_hip(body_fused_prepare(), "hipFuncSetAttribute(fused body LDS)");
-    rt.fused_ready = true;
-  }
-  rt.configured = true;
+  g.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : (g.fused ? 0 : 2);
+  const int low_groups = batch * g.Hl * ((g.Wl + 15) / 16);
+  g.grid.project = clamp_grid(project_num_tiles(batch, g.Hq, g.Wq), project_blocks_per_cu(g.in_fp32, project_precise), cus);
+  g.grid.compress = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(0, mode), cus);
+  g.grid.grouped = clamp_grid(grouped_num_tiles(batch, g.Hl, g.Wl), body_blocks_per_cu(1, mode), cus);
+  g.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, mode), cus);
+  g.grid.refine = clamp_grid(refine_num_tiles(batch, g.Hq, g.Wq), refine_blocks_per_cu(), cus);
+  g.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(g.in_fp32, g.out_fp32), cus);
+  g.body_split = (flags & AEISU_FLAG_BODY_TILE24) ? batch : body_fused_split(mode, batch, g.Hl, g.Wl, cus);
+  g.body_rows16 = (flags & AEISU_FLAG_BODY_TILE24) ? g.Hl : body_fused_row_split(mode, batch, g.Hl, g.Wl, cus);
+  g.grid.fused = clamp_grid(fused_num_tiles(g.in_fp32, batch, height, width, g.Hq, g.Wq, g.py, g.px), 1, cus);
+  return g;
 }
 
 static float inv(float s) { return 1.0f / s; }
 
 // Low-buffer slot written by body layer li (0 compress, 1..4 bottlenecks).
-static int low_slot(const Runtime& rt, int li) { return rt.nlow == 5 ? li : (li % 2); }
+static int low_slot(const Geometry& g, int li) { return g.nlow == 5 ? li : (li % 2); }
 
 // project .. expand (the controller up to the FP16 work tensor); events 0..4
-static void enqueue_body(Runtime& rt, const void* d_in, hipStream_t s, hipEvent_t* ev) {
-  const int m = rt.mode;
+static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in, hipStream_t s,
+                         hipEvent_t* ev) {
+  const int m = w.mode;
   if (ev) check_hip(hipEventRecord(ev[0], s), "hipEventRecord");
-  if (rt.fused_rgb) {
+  if (g.fused_rgb) {
     // analysis + project + compress .. expand in one kernel from the frames, timed as the
     // bottleneck stage (events 0 -> 3; project, compress and expand report zero)
     BodyFusedArgs P{};
     P.frames = d_in;
-    P.work = static_cast<_Float16*>(rt.work.ptr);
-    P.consts = rt.body_consts.as<float>();
-    const LayerDev* layers[6] = {&rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3], &rt.expand};
+    P.work = static_cast<_Float16*>(sc.work);
+    P.consts = w.body_consts.as<float>();
+    const LayerDev* layers[6] = {&w.compress, &w.grouped[0], &w.grouped[1], &w.grouped[2], &w.grouped[3], &w.expand};
     for (int l = 0; l < 6; ++l) {
       P.frag[l] = layers[l]->frag.ptr;
-      P.inv_out[l] = inv(rt.act[l + 2]);
+      P.inv_out[l] = inv(w.act[l + 2]);
     }
-    if (m == 2) P.frag[0] = rt.compress_rgb.ptr;     // INT8: its own frame-input K order
-    P.pfrag = rt.project.frag.ptr;
-    P.inv_in = inv(rt.act[1]);
-    P.s_out = rt.act[7];
-    for (int i = 0; i < 24; ++i) P.analysis[i] = rt.analysis[i];
-    P.Hl = rt.Hl;
-    P.Wl = rt.Wl;
-    P.H = rt.H;
-    P.W = rt.W;
-    P.py = rt.py;
-    P.px = rt.px;
-    const BodySrc src = rt.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
-    const int k = rt.body_split;
+    if (m == 2) P.frag[0] = w.compress_rgb.ptr;     // INT8: its own frame-input K order
+    P.pfrag = w.project.frag.ptr;
+    P.inv_in = inv(w.act[1]);
+    P.s_out = w.act[7];
+    for (int i = 0; i < 24; ++i) P.analysis[i] = w.analysis[i];
+    P.Hl = g.Hl;
+    P.Wl = g.Wl;
+    P.H = g.H;
+    P.W = g.W;
+    P.py = g.py;
+    P.px = g.px;
+    const BodySrc src = g.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
+    const int k = g.body_split;
     if (k > 0) check_hip(launch_body_fused(m, src, P, k, 24, s), "fused body launch");
-    if (k < rt.batch) {                            // trailing frames on 16x16 tiles
+    if (k < g.batch) {                             // trailing frames on 16x16 tiles
       BodyFusedArgs Q = P;
-      Q.frames = static_cast<const char*>(P.frames) + size_t(k) * 3 * rt.H * rt.W * (rt.in_fp32 ? 4 : 2);
-      Q.work = P.work + size_t(k) * rt.Hq * rt.Wq * 32;
-      check_hip(launch_body_fused(m, src, Q, rt.batch - k, 16, s), "fused body launch");
+      Q.frames = static_cast<const char*>(P.frames) + size_t(k) * 3 * g.H * g.W * (g.in_fp32 ? 4 : 2);
+      Q.work = P.work + size_t(k) * g.Hq * g.Wq * 32;
+      check_hip(launch_body_fused(m, src, Q, g.batch - k, 16, s), "fused body launch");
     }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }
-  check_hip(launch_project(rt.in_fp32, rt.project_precise, d_in, rt.project.frag.ptr, rt.project.bias.as<float>(), rt.skip.ptr, rt.analysis,
-                           rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.grid.project, s), "project launch");
+  check_hip(launch_project(g.in_fp32, w.project_precise, d_in, w.project.frag.ptr, w.project.bias.as<float>(), sc.skip,
+                           w.analysis, g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, g.grid.project, s), "project launch");
   if (ev) check_hip(hipEventRecord(ev[1], s), "hipEventRecord");
-  const float* A = rt.act;
-  if (rt.fused) {
+  const float* A = w.act;
+  if (g.fused) {
     // one kernel for compress .. expand, timed as the bottleneck stage (events 1 -> 3;
     // aeisu_stage_timings reports compress and expand as zero on this path)
     BodyFusedArgs P{};
-    P.skip = static_cast<const _Float16*>(rt.skip.ptr);
-    P.work = static_cast<_Float16*>(rt.work.ptr);
-    P.consts = rt.body_consts.as<float>();
-    const LayerDev* layers[6] = {&rt.compress, &rt.grouped[0], &rt.grouped[1], &rt.grouped[2], &rt.grouped[3], &rt.expand};
+    P.skip = static_cast<const _Float16*>(sc.skip);
+    P.work = static_cast<_Float16*>(sc.work);
+    P.consts = w.body_consts.as<float>();
+    const LayerDev* layers[6] = {&w.compress, &w.grouped[0], &w.grouped[1], &w.grouped[2], &w.grouped[3], &w.expand};
     for (int l = 0; l < 6; ++l) {
       P.frag[l] = layers[l]->frag.ptr;
       P.inv_out[l] = m ? inv(A[l + 2]) : 0.f;   // compress s2, bottleneck i s(i+3), expand s7
     }
     P.inv_in = m ? inv(A[1]) : 0.f;
     P.s_out = m ? A[7] : 0.f;
-    P.Hl = rt.Hl;
-    P.Wl = rt.Wl;
-    if (m != 0 || rt.body_rows16 >= rt.Hl) {
-      check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 0, s), "fused body launch");
+    P.Hl = g.Hl;
+    P.Wl = g.Wl;
+    if (m != 0 || g.body_rows16 >= g.Hl) {
+      check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 0, s), "fused body launch");
     } else {                                       // FP16 policy: bottom rows on 8x8 tiles
-      if (rt.body_rows16 > 0) {
+      if (g.body_rows16 > 0) {
         P.row0 = 0;
-        P.rows = rt.body_rows16;
-        check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 16, s), "fused body launch");
+        P.rows = g.body_rows16;
+        check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 16, s), "fused body launch");
       }
-      P.row0 = rt.body_rows16;
-      P.rows = rt.Hl - rt.body_rows16;
-      check_hip(launch_body_fused(m, BodySrc::Skip, P, rt.batch, 8, s), "fused body launch");
+      P.row0 = g.body_rows16;
+      P.rows = g.Hl - g.body_rows16;
+      check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 8, s), "fused body launch");
     }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }
-  check_hip(launch_compress(m, rt.skip.ptr, rt.compress.frag.ptr, rt.compress.bias.as<float>(),
-                            rt.compress.scale.as<float>(), rt.low[low_slot(rt, 0)].ptr, m ? inv(A[1]) : 0.f,
-                            m ? inv(A[2]) : 0.f, rt.Hl, rt.Wl, rt.batch, rt.grid.compress, s), "compress launch");
+  check_hip(launch_compress(m, sc.skip, w.compress.frag.ptr, w.compress.bias.as<float>(), w.compress.scale.as<float>(),
+                            sc.low[low_slot(g, 0)], m ? inv(A[1]) : 0.f, m ? inv(A[2]) : 0.f, g.Hl, g.Wl, g.batch,
+                            g.grid.compress, s), "compress launch");
   if (ev) check_hip(hipEventRecord(ev[2], s), "hipEventRecord");
   for (int i = 0; i < 4; ++i) {
-    check_hip(launch_grouped(m, rt.low[low_slot(rt, i)].ptr, rt.grouped[i].frag.ptr, rt.grouped[i].bias.as<float>(),
-                             rt.grouped[i].scale.as<float>(), rt.low[low_slot(rt, i + 1)].ptr, m ? inv(A[i + 3]) : 0.f,
-                             rt.Hl, rt.Wl, rt.batch, rt.grid.grouped, s), "bottleneck launch");
+    check_hip(launch_grouped(m, sc.low[low_slot(g, i)], w.grouped[i].frag.ptr, w.grouped[i].bias.as<float>(),
+                             w.grouped[i].scale.as<float>(), sc.low[low_slot(g, i + 1)], m ? inv(A[i + 3]) : 0.f,
+                             g.Hl, g.Wl, g.batch, g.grid.grouped, s), "bottleneck launch");
   }
   if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
-  check_hip(launch_expand(m, rt.low[low_slot(rt, 4)].ptr, rt.skip.ptr, rt.expand.frag.ptr, rt.expand.bias.as<float>(),
-                          rt.expand.scale.as<float>(), rt.work.ptr, m ? inv(A[7]) : 0.f, m ? A[7] : 0.f, rt.Hl, rt.Wl,
-                          rt.batch, rt.grid.expand, s), "expand launch");
+  check_hip(launch_expand(m, sc.low[low_slot(g, 4)], sc.skip, w.expand.frag.ptr, w.expand.bias.as<float>(),
+                          w.expand.scale.as<float>(), sc.work, m ? inv(A[7]) : 0.f, m ? A[7] : 0.f, g.Hl, g.Wl,
+                          g.batch, g.grid.expand, s), "expand launch");
   if (ev) check_hip(hipEventRecord(ev[4], s), "hipEventRecord");
 }
 
-static void enqueue_controller(Runtime& rt, const void* d_in, void* d_meta, hipStream_t s, hipEvent_t* ev) {
-  enqueue_body(rt, d_in, s, ev);
-  check_hip(launch_refine_tail(rt.work.ptr, rt.refine_tail.frag.ptr, rt.refine_tail.bias.as<float>(),
-                               rt.tail_bias.as<float>(), d_meta, rt.Hq, rt.Wq, rt.batch, rt.grid.refine, s),
+static void enqueue_controller(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in,
+                               void* d_meta, hipStream_t s, hipEvent_t* ev) {
+  enqueue_body(w, g, sc, d_in, s, ev);
+  check_hip(launch_refine_tail(sc.work, w.refine_tail.frag.ptr, w.refine_tail.bias.as<float>(),
+                               w.tail_bias.as<float>(), d_meta, g.Hq, g.Wq, g.batch, g.grid.refine, s),
             "refine/tail launch");
   if (ev) check_hip(hipEventRecord(ev[5], s), "hipEventRecord");
 }
 
-static void enqueue_head(Runtime& rt, const void* d_in, const void* d_meta, void* d_out, hipStream_t s) {
-  check_hip(launch_head(rt.in_fp32, rt.out_fp32, d_in, d_meta, rt.head.frag.ptr, d_out, rt.H, rt.W, rt.Hq, rt.Wq,
-                        rt.py, rt.px, rt.batch, rt.nonfinite.as<unsigned>(), rt.grid.head, s), "head launch");
+static void enqueue_head(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in,
+                         const void* d_meta, void* d_out, hipStream_t s) {
+  check_hip(launch_head(g.in_fp32, g.out_fp32, d_in, d_meta, w.head.frag.ptr, d_out, g.H, g.W, g.Hq, g.Wq,
+                        g.py, g.px, g.batch, sc.nonfinite, g.grid.head, s), "head launch");
+}
+
+static void enqueue_frame(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in, void* d_out,
+                          hipStream_t s, hipEvent_t* ev) {
+  if (!g.fused) {
+    enqueue_controller(w, g, sc, d_in, sc.meta, s, ev);
+    enqueue_head(w, g, sc, d_in, sc.meta, d_out, s);
+    if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
+    return;
+  }
+  // fused path: events 0, (1,) 3, 6 only; the head stage times refine + tail + head (3 -> 6)
+  enqueue_body(w, g, sc, d_in, s, ev);
+  check_hip(launch_fused_tail_head(g.in_fp32, g.out_fp32, sc.work, d_in, w.refine_tail.frag.ptr,
+                                   w.refine_tail.bias.as<float>(), w.tail_bias.as<float>(), w.head.frag.ptr, d_out,
+                                   g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, g.grid.fused, s),
+            "fused refine/tail/head launch");
+  if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
+}
+
+static std::string startup_report(const Runtime& rt) {
+  const Model& md = *rt.model;
+  const Geometry& g = rt.g;
+  std::ostringstream r;
+  r << "aeisu_amd architecture=" << kArchitecture << " sha256=" << md.art.checksum_hex << " GPU=\"" << md.gpu_name
+    << "\" arch=" << md.gcn_arch << " CUs=" << md.cu_count << " HIP=" << md.hip_runtime_version
+    << " precision=" << precision_name(rt.mode)
+    << " body=" << (g.fused ? (g.fused_rgb ? "fused-analysis-project-compress-4x-grouped-expand"
+                                           : "project+fused-compress-4x-grouped-expand")
+                            : "per-layer-kernels")
+    << " body_mfma=" << (rt.mode == 0 ? "f16" : rt.mode == 1 ? "fp8" : rt.mode == 2 ? "i8" : "f16-on-e4m3-values")
+    << " head=" << (g.fused ? "fused-refine-tail-reconstruction" : "refine-tail+reconstruction")
+    << " source=" << g.W << 'x' << g.H << " batch=" << g.batch << " padded=" << g.Wp << 'x' << g.Hp
+    << " packed=" << g.Wq << 'x' << g.Hq << " low=" << g.Wl << 'x' << g.Hl << " source_pad=" << g.px << ','
+    << g.py << " io=" << (g.in_fp32 ? "f32" : "f16") << '/' << (g.out_fp32 ? "f32" : "f16")
+    << " body_tiles24_frames=" << g.body_split << " weights_bytes=" << rt.w->bytes()
+    << " scratch_bytes=" << rt.scratch_bytes() << " shared_model_users=" << rt.model.use_count();
+  return r.str();
+}
+
+static void configure(Runtime& rt, int batch, int height, int width, int in_layout, int out_layout, int precision,
+                      unsigned flags) {
+  const int mode = precision ? mode_of(precision) : rt.mode;
+  const ModeWeights& w = rt.model->weights(mode);
+  Geometry g = make_geometry(mode, w.project_precise, rt.model->cu_count, batch, height, width, in_layout, out_layout,
+                             flags);
+  rt.drop_graph();
+  rt.configured = false;
+  rt.timed_frames = 0;                 // recorded stage events belong to the previous layout
+  rt.skip.alloc(g.skip_bytes());
+  rt.work.alloc(g.work_bytes());
+  rt.meta.alloc(g.meta_bytes());
+  for (int i = 0; i < 5; ++i) rt.low[i].alloc(i < g.nlow ? g.lowpx() * 64 * (mode == 0 ? 2 : 1) : 0);
+  rt.nonfinite.alloc(4);
+  check_hip(hipMemset(rt.nonfinite.ptr, 0, 4), "hipMemset(flag)");
+  if (precision) rt.precision = precision;
+  rt.mode = mode;
+  rt.w = &w;
+  rt.g = g;
+  rt.configured = true;
+  rt.report = startup_report(rt);
 }
 
 static hipEvent_t* next_events(Runtime& rt) {
-  if (!(rt.flags & AEISU_FLAG_STAGE_TIMING) || rt.timed_frames >= kMaxTimedFrames) return nullptr;
+  if (!(rt.g.flags & AEISU_FLAG_STAGE_TIMING) || rt.timed_frames >= kMaxTimedFrames) return nullptr;
   const size_t need = size_t(rt.timed_frames + 1) * kStageEvents;
   while (rt.events.size() < need) {
     hipEvent_t e;
@@ -773,23 +928,6 @@ static hipEvent_t* next_events(Runtime& rt) {
     rt.events.push_back(e);
   }
   return &rt.events[size_t(rt.timed_frames++) * kStageEvents];
-}
-
-static void enqueue_frame(Runtime& rt, const void* d_in, void* d_out, hipStream_t s, hipEvent_t* ev) {
-  if (!rt.fused) {
-    enqueue_controller(rt, d_in, rt.meta.ptr, s, ev);
-    enqueue_head(rt, d_in, rt.meta.ptr, d_out, s);
-    if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
-    return;
-  }
-  // fused path: events 0, (1,) 3, 6 only; the head stage times refine + tail + head (3 -> 6)
-  enqueue_body(rt, d_in, s, ev);
-  check_hip(launch_fused_tail_head(rt.in_fp32, rt.out_fp32, rt.work.ptr, d_in, rt.refine_tail.frag.ptr,
-                                   rt.refine_tail.bias.as<float>(), rt.tail_bias.as<float>(), rt.head.frag.ptr, d_out,
-                                   rt.H, rt.W, rt.Hq, rt.Wq, rt.py, rt.px, rt.batch, rt.nonfinite.as<unsigned>(),
-                                   rt.grid.fused, s),
-            "fused refine/tail/head launch");
-  if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
 }
 
 static void require_configured(const Runtime& rt) {
@@ -830,7 +968,7 @@ static int guarded(Fn fn) {
 
 static Runtime& runtime_of(aeisu_runtime* rt) {
   if (!rt || !rt->impl) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null runtime handle");
-  aeisu::check_hip(hipSetDevice(rt->impl->device), "hipSetDevice");
+  aeisu::check_hip(hipSetDevice(rt->impl->model->device), "hipSetDevice");
   return *rt->impl;
 }
 
@@ -839,26 +977,28 @@ static int create_impl(const uint8_t* data, size_t size, int precision, aeisu_ru
     if (!out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output handle");
     *out = nullptr;
     if (!data || size == 0) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "empty artifact");
-    if (precision != AEISU_PRECISION_FP16 && precision != AEISU_PRECISION_MIXED &&
-        precision != AEISU_PRECISION_INT8 && precision != AEISU_PRECISION_MIXED_FP8MMA)
-      aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "unknown precision");
-    auto rt = std::make_unique<Runtime>();
-    rt->precision = precision;
-    // kernel modes: 0 FP16, 1 E4M3 on the FP8 MFMA, 2 INT8, 3 E4M3 values on the FP16 MFMA
-    rt->mode = precision == AEISU_PRECISION_FP16 ? 0
-               : precision == AEISU_PRECISION_MIXED ? 3
-               : precision == AEISU_PRECISION_MIXED_FP8MMA ? 1 : 2;
+    const int mode = aeisu::mode_of(precision);
+    auto model = std::make_shared<aeisu::Model>();
+    model->art = aeisu::parse_artifact(data, size);   // host-only validation before any HIP call
     {
-      // host-only: parse, validate and pack every tensor before touching the device
-      aeisu::Artifact art = aeisu::parse_artifact(data, size);
-      rt->checksum = art.checksum_hex;
-      aeisu::upload_weights(*rt, art);
+      // pack (and so validate) the requested policy's tensors on the host first
+      aeisu::ModeWeights probe;
+      probe.mode = mode;
+      aeisu::pack_weights(probe, model->art);
     }
-    aeisu::check_hip(hipGetDevice(&rt->device), "hipGetDevice");
+    aeisu::check_hip(hipGetDevice(&model->device), "hipGetDevice");
     hipDeviceProp_t prop;
-    aeisu::check_hip(hipGetDeviceProperties(&prop, rt->device), "hipGetDeviceProperties");
-    rt->cu_count = prop.multiProcessorCount;
-    aeisu::commit_weights(*rt);
+    aeisu::check_hip(hipGetDeviceProperties(&prop, model->device), "hipGetDeviceProperties");
+    model->cu_count = prop.multiProcessorCount;
+    model->gpu_name = prop.name;
+    model->gcn_arch = prop.gcnArchName;
+    aeisu::check_hip(hipRuntimeGetVersion(&model->hip_runtime_version), "hipRuntimeGetVersion");
+    aeisu::prepare_device(model->device);
+    auto rt = std::make_unique<Runtime>();
+    rt->model = model;
+    rt->precision = precision;
+    rt->mode = mode;
+    rt->w = &model->weights(mode);
     auto* h = new aeisu_runtime;
     h->impl = std::move(rt);
     *out = h;
@@ -890,8 +1030,32 @@ int aeisu_create_from_file(const char* path, int precision, aeisu_runtime** out)
   return create_impl(bytes.data(), bytes.size(), precision, out);
 }
 
-int aeisu_configure(aeisu_runtime* h, int batch, int height, int width, int in_layout, int out_layout, unsigned flags) {
-  return guarded([&] { aeisu::configure(runtime_of(h), batch, height, width, in_layout, out_layout, flags); });
+int aeisu_create_sibling(const aeisu_runtime* src, aeisu_runtime** out) {
+  return guarded([&] {
+    if (!out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null output handle");
+    *out = nullptr;
+    if (!src || !src->impl) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null runtime handle");
+    const Runtime& s = *src->impl;
+    auto rt = std::make_unique<Runtime>();
+    rt->model = s.model;
+    rt->precision = s.precision;
+    rt->mode = s.mode;
+    rt->w = s.w;
+    auto* h = new aeisu_runtime;
+    h->impl = std::move(rt);
+    *out = h;
+  });
+}
+
+int aeisu_shares_weights(const aeisu_runtime* a, const aeisu_runtime* b) {
+  return a && b && a->impl && b->impl && a->impl->model == b->impl->model;
+}
+
+int aeisu_configure(aeisu_runtime* h, int batch, int height, int width, int in_layout, int out_layout, int precision,
+                    unsigned flags) {
+  return guarded([&] {
+    aeisu::configure(runtime_of(h), batch, height, width, in_layout, out_layout, precision, flags);
+  });
 }
 
 int aeisu_upscale_async(aeisu_runtime* h, const void* d_in, void* d_out, void* stream) {
@@ -899,7 +1063,7 @@ int aeisu_upscale_async(aeisu_runtime* h, const void* d_in, void* d_out, void* s
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
     if (!d_in || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null frame buffer");
-    aeisu::enqueue_frame(rt, d_in, d_out, (hipStream_t)stream, aeisu::next_events(rt));
+    aeisu::enqueue_frame(*rt.w, rt.g, rt.scratch(), d_in, d_out, (hipStream_t)stream, aeisu::next_events(rt));
   });
 }
 
@@ -943,7 +1107,7 @@ int aeisu_upscale_graph(aeisu_runtime* h, const void* d_in, void* d_out, void* s
       aeisu::check_hip(hipStreamBeginCapture(rt.capture_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
       hipGraph_t graph = nullptr;
       try {
-        aeisu::enqueue_frame(rt, d_in, d_out, rt.capture_stream, nullptr);
+        aeisu::enqueue_frame(*rt.w, rt.g, rt.scratch(), d_in, d_out, rt.capture_stream, nullptr);
       } catch (...) {
         (void)hipStreamEndCapture(rt.capture_stream, &graph);
         if (graph) (void)hipGraphDestroy(graph);
@@ -966,7 +1130,7 @@ int aeisu_controller_async(aeisu_runtime* h, const void* d_in, void* d_meta, voi
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
     if (!d_in || !d_meta) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null buffer");
-    aeisu::enqueue_controller(rt, d_in, d_meta, (hipStream_t)stream, nullptr);
+    aeisu::enqueue_controller(*rt.w, rt.g, rt.scratch(), d_in, d_meta, (hipStream_t)stream, nullptr);
   });
 }
 
@@ -975,17 +1139,17 @@ int aeisu_head_async(aeisu_runtime* h, const void* d_in, const void* d_meta, voi
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
     if (!d_in || !d_meta || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null buffer");
-    aeisu::enqueue_head(rt, d_in, d_meta, d_out, (hipStream_t)stream);
+    aeisu::enqueue_head(*rt.w, rt.g, rt.scratch(), d_in, d_meta, d_out, (hipStream_t)stream);
   });
 }
 
 size_t aeisu_intermediate_bytes(const aeisu_runtime* h, int which) {
   if (!h || !h->impl || !h->impl->configured) return 0;
   const Runtime& rt = *h->impl;
-  const size_t packed = size_t(rt.batch) * rt.Hq * rt.Wq, lowpx = size_t(rt.batch) * rt.Hl * rt.Wl;
+  const size_t packed = rt.g.packed(), lowpx = rt.g.lowpx();
   if (which == AEISU_BUF_SKIP || which == AEISU_BUF_WORK) return packed * 64;
   if (which == AEISU_BUF_META) return packed * 128;
-  if (which >= AEISU_BUF_LOW0 && which <= AEISU_BUF_LOW4) return lowpx * 64 * rt.low_elem();
+  if (which >= AEISU_BUF_LOW0 && which <= AEISU_BUF_LOW4) return lowpx * 64 * (rt.mode == 0 ? 2 : 1);
   return 0;
 }
 
@@ -1010,11 +1174,11 @@ int aeisu_copy_intermediate(aeisu_runtime* h, int which, void* d_dst, size_t byt
       src = rt.meta.ptr;
     } else {
       const int li = which - AEISU_BUF_LOW0;
-      if (rt.nlow == 0)
+      if (rt.g.nlow == 0)
         aeisu::fail(AEISU_ERR_STATE, "the fused body keeps activations on chip; configure with "
                                      "AEISU_FLAG_UNFUSED or AEISU_FLAG_KEEP_INTERMEDIATES to read them");
-      if (rt.nlow != 5 && li != 4) aeisu::fail(AEISU_ERR_STATE, "configure with AEISU_FLAG_KEEP_INTERMEDIATES to read this layer");
-      src = rt.low[aeisu::low_slot(rt, li)].ptr;
+      if (rt.g.nlow != 5 && li != 4) aeisu::fail(AEISU_ERR_STATE, "configure with AEISU_FLAG_KEEP_INTERMEDIATES to read this layer");
+      src = rt.low[aeisu::low_slot(rt.g, li)].ptr;
     }
     aeisu::check_hip(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream), "hipMemcpyAsync");
   });
@@ -1025,7 +1189,8 @@ int aeisu_geometry(const aeisu_runtime* h, int out[6]) {
     if (!h || !h->impl || !out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null argument");
     const Runtime& rt = *h->impl;
     aeisu::require_configured(rt);
-    out[0] = rt.Hp; out[1] = rt.Wp; out[2] = rt.py; out[3] = rt.px; out[4] = rt.Hq; out[5] = rt.Wq;
+    const aeisu::Geometry& g = rt.g;
+    out[0] = g.Hp; out[1] = g.Wp; out[2] = g.py; out[3] = g.px; out[4] = g.Hq; out[5] = g.Wq;
   });
 }
 
@@ -1040,8 +1205,8 @@ int aeisu_stage_timings(aeisu_runtime* h, float ms[AEISU_STAGE_COUNT], int* fram
     static const int per_layer_from[6] = {0, 1, 2, 3, 4, 5}, per_layer_to[6] = {1, 2, 3, 4, 5, 6};
     static const int fused_from[6] = {0, -1, 1, -1, -1, 3}, fused_to[6] = {1, -1, 3, -1, -1, 6};
     static const int rgb_from[6] = {-1, -1, 0, -1, -1, 3}, rgb_to[6] = {-1, -1, 3, -1, -1, 6};
-    const int* from = rt.fused_rgb ? rgb_from : rt.fused ? fused_from : per_layer_from;
-    const int* to = rt.fused_rgb ? rgb_to : rt.fused ? fused_to : per_layer_to;
+    const int* from = rt.g.fused_rgb ? rgb_from : rt.g.fused ? fused_from : per_layer_from;
+    const int* to = rt.g.fused_rgb ? rgb_to : rt.g.fused ? fused_to : per_layer_to;
     for (int f = 0; f < rt.timed_frames; ++f) {
       hipEvent_t* e = &rt.events[size_t(f) * aeisu::kStageEvents];
       aeisu::check_hip(hipEventSynchronize(e[6]), "hipEventSynchronize");
@@ -1067,19 +1232,24 @@ int aeisu_reset_timings(aeisu_runtime* h) {
 size_t aeisu_persistent_bytes(const aeisu_runtime* h) {
   if (!h || !h->impl) return 0;
   const Runtime& rt = *h->impl;
-  size_t n = rt.project.frag.bytes + rt.project.bias.bytes + rt.compress.frag.bytes + rt.compress.bias.bytes +
-             rt.compress.scale.bytes + rt.expand.frag.bytes + rt.expand.bias.bytes + rt.expand.scale.bytes +
-             rt.refine_tail.frag.bytes + rt.refine_tail.bias.bytes + rt.tail_bias.bytes + rt.head.frag.bytes +
-             rt.skip.bytes + rt.work.bytes + rt.meta.bytes + rt.nonfinite.bytes;
-  for (const auto& g : rt.grouped) n += g.frag.bytes + g.bias.bytes + g.scale.bytes;
-  for (const auto& l : rt.low) n += l.bytes;
-  return n;
+  return rt.model->bytes() + rt.scratch_bytes();
+}
+
+size_t aeisu_startup_report(const aeisu_runtime* h, char* out, size_t capacity) {
+  if (!h || !h->impl || !h->impl->configured) return 0;
+  const std::string& r = h->impl->report;
+  if (out && capacity) {
+    const size_t n = std::min(capacity - 1, r.size());
+    std::memcpy(out, r.data(), n);
+    out[n] = '\0';
+  }
+  return r.size() + 1;
 }
 
 int aeisu_artifact_checksum(const aeisu_runtime* h, char out[65]) {
   return guarded([&] {
     if (!h || !h->impl || !out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null argument");
-    std::snprintf(out, 65, "%s", h->impl->checksum.c_str());
+    std::snprintf(out, 65, "%s", h->impl->model->art.checksum_hex.c_str());
   });
 }
 
@@ -1087,6 +1257,6 @@ void aeisu_destroy(aeisu_runtime* h) { delete h; }
 
 const char* aeisu_last_error(void) { return g_last_error.c_str(); }
 
-const char* aeisu_version(void) { return "aeisu_amd 0.1.0 (gfx950)"; }
+const char* aeisu_version(void) { return "aeisu_amd 0.2.0 (gfx950)"; }
 
 }  // extern "C"

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 from pathlib import Path
+from collections import OrderedDict
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -30,19 +31,33 @@ def _stream_ptr(stream: Optional[torch.cuda.Stream]) -> int:
 
 
 class _Handle:
-    """One native runtime configured for one (batch, H, W, layouts, flags)."""
+    """One native runtime configured for one (batch, H, W, layouts, flags).
 
-    def __init__(self, blob: bytes, precision: str):
+    The first handle of an Upscaler loads the artifact; every further one is a sibling
+    (aeisu_create_sibling) that shares its uploaded weights and owns only its scratch.
+    """
+
+    def __init__(self, precision: str, blob: Optional[bytes] = None, sibling_of: Optional["_Handle"] = None):
         self.ptr = ctypes.c_void_p()
-        buf = ctypes.create_string_buffer(blob, len(blob))
-        L.check(L.lib().aeisu_create_from_memory(buf, len(blob), L.PRECISION[precision], ctypes.byref(self.ptr)))
+        self.precision = precision
+        if sibling_of is not None:
+            L.check(L.lib().aeisu_create_sibling(sibling_of.ptr, ctypes.byref(self.ptr)))
+        else:
+            buf = ctypes.create_string_buffer(blob, len(blob))
+            L.check(L.lib().aeisu_create_from_memory(buf, len(blob), L.PRECISION[precision], ctypes.byref(self.ptr)))
         self.key = None
 
     def configure(self, key) -> None:
         if key != self.key:
             batch, h, w, lin, lout, flags = key
-            L.check(L.lib().aeisu_configure(self.ptr, batch, h, w, lin, lout, flags))
+            L.check(L.lib().aeisu_configure(self.ptr, batch, h, w, lin, lout, L.PRECISION[self.precision], flags))
             self.key = key
+
+    def report(self) -> str:
+        n = L.lib().aeisu_startup_report(self.ptr, None, 0)
+        buf = ctypes.create_string_buffer(max(int(n), 1))
+        L.lib().aeisu_startup_report(self.ptr, buf, len(buf))
+        return buf.value.decode()
 
     def close(self) -> None:
         if self.ptr:
@@ -61,32 +76,51 @@ class Upscaler:
 
     The reference counterparts are ``FoldedAEISU`` (aeisu/model.py:554-596)
     for the Python path and ``aess::srcpyr::CudaRuntime``
-    (SrcPyrCudaRuntime.h:29-96) for the native one.
+    (SrcPyrCudaRuntime.h:29-96) for the native one.  The artifact is parsed and
+    its weights uploaded once; each frame geometry gets a sibling runtime with
+    its own scratch, and at most ``max_handles`` geometries are kept (least
+    recently used first out), so tiled or mixed-size workloads do not grow
+    device memory without bound.
     """
 
-    def __init__(self, blob: bytes, precision: str, device: str = "cuda"):
+    def __init__(self, blob: bytes, precision: str, device: str = "cuda", max_handles: int = 8):
         if precision not in L.PRECISION:
             raise ValueError(f"precision must be one of {sorted(L.PRECISION)}")
         dev = torch.device(device)
         if dev.type != "cuda" or not torch.cuda.is_available():
             raise ValueError("the AEISU MI355X runtime needs a HIP device (device='cuda')")
         self.device = torch.device("cuda", dev.index if dev.index is not None else torch.cuda.current_device())
-        self.blob, self.precision = blob, precision
-        self._handles: Dict[Tuple, _Handle] = {}
+        self.precision = precision
+        self.max_handles = max(1, max_handles)
+        self._handles: "OrderedDict[Tuple, _Handle]" = OrderedDict()
         with torch.cuda.device(self.device):
-            self._main = _Handle(blob, precision)     # validates the artifact eagerly
+            self._main = _Handle(precision, blob=blob)     # validates the artifact and uploads once
 
     # -- handles ---------------------------------------------------------------------------
     def handle(self, batch: int, h: int, w: int, in_dtype=torch.float16, out_dtype=torch.float16,
                flags: int = 0) -> _Handle:
         key = (batch, h, w, _DTYPES[in_dtype], _DTYPES[out_dtype], flags)
         hd = self._handles.get(key)
-        if hd is None:
-            with torch.cuda.device(self.device):
-                hd = self._main if self._main.key is None else _Handle(self.blob, self.precision)
-                hd.configure(key)
-            self._handles[key] = hd
+        if hd is not None:
+            self._handles.move_to_end(key)
+            return hd
+        with torch.cuda.device(self.device):
+            if len(self._handles) >= self.max_handles:
+                _, old = self._handles.popitem(last=False)
+                if old is not self._main:
+                    old.close()
+                else:
+                    old.key = None
+            hd = self._main if self._main.key is None else _Handle(self.precision, sibling_of=self._main)
+            hd.configure(key)
+        self._handles[key] = hd
         return hd
+
+    def report(self, hd: Optional[_Handle] = None) -> str:
+        """Startup report of a configured handle (default: the most recently configured one)."""
+        if hd is None:
+            hd = next(reversed(self._handles.values()))
+        return hd.report()
 
     def _check_frames(self, frames: torch.Tensor) -> None:
         if frames.ndim != 4 or frames.shape[1] != 3:
@@ -164,8 +198,15 @@ class Upscaler:
         return dict(zip(L.STAGES, list(ms))), frames.value
 
     def persistent_bytes(self) -> int:
-        return sum(int(L.lib().aeisu_persistent_bytes(h.ptr)) for h in {id(h): h for h in
-                                                                       [self._main, *self._handles.values()]}.values())
+        """Uploaded weights (shared by every handle) plus every live handle's scratch: a handle reports
+        weights + its scratch, an unconfigured sibling the weights alone."""
+        probe = _Handle(self.precision, sibling_of=self._main)
+        try:
+            weights = int(L.lib().aeisu_persistent_bytes(probe.ptr))
+        finally:
+            probe.close()
+        handles = {id(h): h for h in [self._main, *self._handles.values()] if h.ptr}.values()
+        return weights + sum(int(L.lib().aeisu_persistent_bytes(h.ptr)) - weights for h in handles)
 
     def checksum(self) -> str:
         out = ctypes.create_string_buffer(65)
@@ -176,6 +217,12 @@ class Upscaler:
         for h in list(self._handles.values()) + [self._main]:
             h.close()
         self._handles.clear()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def load_model(path, device: str = "cuda", precision: Optional[str] = None) -> Upscaler:

@@ -78,20 +78,32 @@ extern "C" {
 
 typedef struct aeisu_runtime aeisu_runtime;
 
-/* Load and validate an artifact and upload its weights to the current HIP device.
+/* Load and validate an artifact and upload the weights of `precision` to the current HIP device.
  * Replaces CudaRuntime(modelPath) -> ModelArtifact::Load + UploadModel
  * (SrcPyrCudaRuntime.cu:5380-5383, 2924-3170; SrcPyrModel.cpp:243-470).
  * The artifact is SPYR8F8 (SrcPyrModel.cpp:37-81); FP16 needs the *.weight_fp16
  * tensors, MIXED the *.weight_fp8 / weight_scale / bias_fp8 / activation_scales
- * tensors, INT8 the *.weight_i8 / int8_factor tensors (data type 6). */
+ * tensors, INT8 the *.weight_i8 / int8_factor tensors (data type 6).  `precision`
+ * is the policy the runtime runs until aeisu_configure names another one. */
 int aeisu_create_from_file(const char* path, int precision, aeisu_runtime** out);
 int aeisu_create_from_memory(const void* data, size_t size, int precision, aeisu_runtime** out);
 
-/* Fix the frame geometry and allocate scratch.  Replaces Configure(...)
- * (SrcPyrCudaRuntime.cu:5071-5133) with device-buffer layouts instead of
- * D3D11 textures.  Rejects zero or > 8192 dimensions (SrcPyrRuntimeTest.cpp:302-303). */
+/* A new runtime that shares `src`'s loaded artifact and uploaded weights (no parse, no upload) and
+ * has its own configuration, scratch and timing: one weight upload serves several frame geometries.
+ * Replaces CudaRuntime::CreateSibling (SrcPyrCudaRuntime.h:38, .cu:5392-5396).  The weights stay
+ * alive while any runtime sharing them exists; destroy each runtime with aeisu_destroy. */
+int aeisu_create_sibling(const aeisu_runtime* src, aeisu_runtime** out);
+
+/* 1 if the two runtimes share their weights (SharesExecutionEngineWith, SrcPyrCudaRuntime.h:39), else 0. */
+int aeisu_shares_weights(const aeisu_runtime* a, const aeisu_runtime* b);
+
+/* Fix the frame geometry and policy and allocate scratch.  Replaces Configure(...)
+ * (SrcPyrCudaRuntime.h:41, .cu:5071-5133) with device-buffer layouts instead of D3D11 textures.
+ * `precision` (AEISU_PRECISION_*, or 0 to keep the runtime's current one) selects the policy; its
+ * weights are uploaded on first use and shared with siblings.  Rejects zero or > 8192 dimensions
+ * (SrcPyrRuntimeTest.cpp:302-303) and a policy the artifact has no tensors for. */
 int aeisu_configure(aeisu_runtime* rt, int batch, int height, int width, int in_layout, int out_layout,
-                    unsigned flags);
+                    int precision, unsigned flags);
 
 /* Enqueue one batch: d_in [B][3][H][W] -> d_out [B][3][2H][2W], clipped to [0,1].
  * Asynchronous on `stream` (a hipStream_t, NULL = default stream).  Replaces
@@ -132,8 +144,14 @@ int aeisu_geometry(const aeisu_runtime* rt, int out[6]);
 int aeisu_stage_timings(aeisu_runtime* rt, float ms[AEISU_STAGE_COUNT], int* frames);
 int aeisu_reset_timings(aeisu_runtime* rt);
 
-/* Device bytes held by the runtime (weights + scratch).  Replaces PersistentDeviceBytes. */
+/* Device bytes held by the runtime: every uploaded weight buffer of its (shared) model plus its own
+ * scratch.  Replaces PersistentDeviceBytes (SrcPyrCudaRuntime.h:79). */
 size_t aeisu_persistent_bytes(const aeisu_runtime* rt);
+
+/* One-line description of the configuration (artifact hash, GPU, policy, kernels, geometry, bytes),
+ * NUL-terminated into out[0..capacity).  Returns the size needed including the NUL (0 if the runtime
+ * is not configured).  Replaces StartupReport (SrcPyrCudaRuntime.h:78, .cu:3740-3783). */
+size_t aeisu_startup_report(const aeisu_runtime* rt, char* out, size_t capacity);
 
 /* Artifact SHA-256 as 64 hex characters + NUL (ModelArtifact::ChecksumHex). */
 int aeisu_artifact_checksum(const aeisu_runtime* rt, char out[65]);

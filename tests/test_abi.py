@@ -178,12 +178,15 @@ def test_semantic_validation(blobs, case, prec, expect):
 
 def test_argument_validation_without_device():
     lib = L.lib()
-    assert lib.aeisu_configure(None, 1, 8, 8, 0, 0, 0) == L.AEISU_ERR_INVALID_ARGUMENT
+    assert lib.aeisu_configure(None, 1, 8, 8, 0, 0, 0, 0) == L.AEISU_ERR_INVALID_ARGUMENT
     assert b"null runtime" in lib.aeisu_last_error()
     h = ctypes.c_void_p()
     assert lib.aeisu_create_from_memory(b"x", 1, 99, ctypes.byref(h)) == L.AEISU_ERR_INVALID_ARGUMENT
     assert lib.aeisu_create_from_file(b"/nonexistent/model.bin", 2, ctypes.byref(h)) == L.AEISU_ERR_ARTIFACT
     assert lib.aeisu_intermediate_bytes(None, 0) == 0 and lib.aeisu_persistent_bytes(None) == 0
+    assert lib.aeisu_create_sibling(None, ctypes.byref(h)) == L.AEISU_ERR_INVALID_ARGUMENT and not h.value
+    assert lib.aeisu_shares_weights(None, None) == 0
+    assert lib.aeisu_startup_report(None, None, 0) == 0
 
 
 def test_header_layout_constants():

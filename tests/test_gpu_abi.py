@@ -1,0 +1,76 @@
+"""The public C header driven from compiled code and the Python shim's handle cache, on the GPU.
+
+* tests/abi_smoke (built from tests/abi_smoke.cpp by aeisu_amd/build.py) includes
+  include/aeisu_amd.h and runs create -> configure -> upscale -> destroy, a weight-sharing
+  sibling, a precision change at configure, the startup report, a non-finite input and the
+  error codes, as a native caller of the reference's CudaRuntime would.
+* Upscaler uploads the weights once and serves further geometries from sibling runtimes,
+  bounded by an LRU of handles.
+"""
+from __future__ import annotations
+
+import subprocess
+import sys
+
+import pytest
+import torch
+
+from tests._util import ROOT, WEIGHTS
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_compiled_cpp_caller(gpu):
+    exe = ROOT / "tests" / "abi_smoke"
+    if not exe.exists():
+        pytest.fail("tests/abi_smoke is not built; run `python -m aeisu_amd.build`")
+    say("case: tests/abi_smoke (C++ caller of include/aeisu_amd.h)")
+    artifact = WEIGHTS / "aeisu_area_mixed_fp8.bin"
+    stored = artifact.read_bytes()[184:216].hex()        # SHA-256 field of the SPYR8F8 header
+    res = subprocess.run([str(exe), str(artifact), stored], capture_output=True, text=True, timeout=120)
+    say(res.stdout)
+    assert res.returncode == 0 and "abi_smoke: OK" in res.stdout, res.stdout + res.stderr
+
+
+def test_upscaler_shares_weights_and_bounds_handles(gpu):
+    from aeisu_amd import _lib as L
+    from aeisu_amd import frames
+    from aeisu_amd import runtime as R
+    say("case: Upscaler sibling handles and LRU bound")
+    model = R.load_model(WEIGHTS / "aeisu_area_mixed_fp8.bin", precision="mixed")
+    model.max_handles = 2
+    shapes = [(40, 56), (64, 96), (72, 104), (40, 56)]
+    outs = []
+    for h, w in shapes:
+        x = frames.scene(h, w, h + w, shapes=5, texture=True).half()[None].cuda().contiguous()
+        outs.append(model.run(x))
+    torch.cuda.synchronize()
+    assert len(model._handles) == 2
+    live = [hd for hd in model._handles.values()]
+    assert all(L.lib().aeisu_shares_weights(model._main.ptr, hd.ptr) == 1 for hd in live)
+    report = model.report()
+    say(f"  {report}")
+    assert "precision=FP8/FP16-Mixed" in report and "shared_model_users=" in report
+    # a fresh model gives the same results: sharing changes nothing numerically
+    fresh = R.load_model(WEIGHTS / "aeisu_area_mixed_fp8.bin", precision="mixed")
+    for (h, w), got in zip(shapes, outs):
+        x = frames.scene(h, w, h + w, shapes=5, texture=True).half()[None].cuda().contiguous()
+        assert torch.equal(fresh.run(x), got)
+    # weights are counted once: the two live handles hold the weights plus each its own scratch
+    import ctypes
+    bare = ctypes.c_void_p()
+    L.check(L.lib().aeisu_create_sibling(model._main.ptr, ctypes.byref(bare)))
+    weights = int(L.lib().aeisu_persistent_bytes(bare))
+    L.lib().aeisu_destroy(bare)
+    per_handle = [int(L.lib().aeisu_persistent_bytes(hd.ptr)) for hd in live]
+    total = model.persistent_bytes()
+    say(f"  persistent bytes: weights {weights}, handles {per_handle}, model total {total}")
+    assert all(b > weights for b in per_handle)
+    assert total == weights + sum(b - weights for b in per_handle)
+    model.close()
+    fresh.close()
