@@ -32,6 +32,7 @@ SIGNATURES = {
     "aeisu_create_sibling": (_I, [_P, ctypes.POINTER(_P)]),
     "aeisu_shares_weights": (_I, [_P, _P]),
     "aeisu_configure": (_I, [_P, _I, _I, _I, _I, _I, _I, _U]),
+    "aeisu_upscale_noalloc": (_I, [_P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "aeisu_startup_report": (_S, [_P, ctypes.c_char_p, _S]),
     "aeisu_upscale_async": (_I, [_P, _P, _P, _P]),
     "aeisu_upscale": (_I, [_P, _P, _P, _P]),

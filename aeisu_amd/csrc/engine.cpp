@@ -662,7 +662,8 @@ static void commit_weights(ModeWeights& w) {
   w.each_buffer([](DeviceBuffer& b) { b.commit(); });
 }
 
-// Per-device set-up that every launch path needs: the fused kernels' LDS limits.
+// Per-device set-up that every launch path needs: the fused kernels' LDS limits, and the address of
+// the library's static scratch array (defined with the allocation-free entry point in noalloc.hip).
 static std::mutex g_prepare_mu;
 static bool g_prepared[64];
 static void prepare_device(int device) {
@@ -671,6 +672,7 @@ static void prepare_device(int device) {
   if (g_prepared[device]) return;
   check_hip(fused_prepare(), "hipFuncSetAttribute(fused LDS)");
   check_hip(body_fused_prepare(), "hipFuncSetAttribute(fused body LDS)");
+  check_hip(noalloc_scratch_init(device), "hipGetSymbolAddress(scratch)");
   g_prepared[device] = true;
 }
 
@@ -934,6 +936,27 @@ static void require_configured(const Runtime& rt) {
   if (!rt.configured) fail(AEISU_ERR_STATE, "runtime is not configured");
 }
 
+// The default (fused) path on the static scratch array: geometry on the stack, no allocation.
+// Scratch layout: [0, 256) non-finite flag, then the skip tensor (FP16 policy) and the work tensor,
+// each 256-byte aligned.
+static void enqueue_noalloc(const Runtime& rt, int batch, int height, int width, int in_layout, int out_layout,
+                            const void* d_in, void* d_out, hipStream_t s) {
+  const Geometry g = make_geometry(rt.mode, rt.w->project_precise, rt.model->cu_count, batch, height, width,
+                                   in_layout, out_layout, 0);
+  auto up = [](size_t n) { return (n + 255) & ~size_t(255); };
+  const size_t need = 256 + up(g.skip_bytes()) + up(g.work_bytes());
+  if (need > kNoAllocScratchBytes)
+    fail(AEISU_ERR_INVALID_ARGUMENT, "frame needs " + std::to_string(need) + " bytes of scratch; the allocation-free "
+                                     "entry point has " + std::to_string(kNoAllocScratchBytes));
+  char* base = static_cast<char*>(noalloc_scratch(rt.model->device));
+  if (!base) fail(AEISU_ERR_STATE, "static scratch was not set up on this device");
+  Scratch sc;
+  sc.nonfinite = reinterpret_cast<unsigned*>(base);
+  sc.skip = g.skip_bytes() ? base + 256 : nullptr;
+  sc.work = base + 256 + up(g.skip_bytes());
+  enqueue_frame(*rt.w, g, sc, d_in, d_out, s, nullptr);
+}
+
 }  // namespace aeisu
 
 // ================================================================================================
@@ -1064,6 +1087,15 @@ int aeisu_upscale_async(aeisu_runtime* h, const void* d_in, void* d_out, void* s
     aeisu::require_configured(rt);
     if (!d_in || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null frame buffer");
     aeisu::enqueue_frame(*rt.w, rt.g, rt.scratch(), d_in, d_out, (hipStream_t)stream, aeisu::next_events(rt));
+  });
+}
+
+int aeisu_upscale_noalloc(aeisu_runtime* h, int batch, int height, int width, int in_layout, int out_layout,
+                          const void* d_in, void* d_out, void* stream) {
+  return guarded([&] {
+    Runtime& rt = runtime_of(h);
+    if (!d_in || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null frame buffer");
+    aeisu::enqueue_noalloc(rt, batch, height, width, in_layout, out_layout, d_in, d_out, (hipStream_t)stream);
   });
 }
 

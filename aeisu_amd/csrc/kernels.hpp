@@ -81,4 +81,12 @@ int project_blocks_per_cu(int in_fp32, int precise);
 int refine_blocks_per_cu();
 int body_blocks_per_cu(int kind, int mode);   // kind 0 compress, 1 grouped, 2 expand
 
+// Static scratch of the allocation-free entry point (noalloc.hip): 72 MiB per device, enough for the
+// work tensor (and the FP16 policy's skip tensor) of one 1920x1080 frame in every policy.
+constexpr size_t kNoAllocScratchBytes = size_t(72) << 20;
+// Once per device, with that device current: looks up the array's device address.
+hipError_t noalloc_scratch_init(int device);
+// The array's device address on `device` (nullptr before noalloc_scratch_init succeeded there).
+void* noalloc_scratch(int device);
+
 }  // namespace aeisu

@@ -121,6 +121,17 @@ int aeisu_upscale(aeisu_runtime* rt, const void* d_in, void* d_out, void* stream
  * reference's pre-captured CUDA graph launch (SrcPyrCudaRuntime.cu:4959-5028). */
 int aeisu_upscale_graph(aeisu_runtime* rt, const void* d_in, void* d_out, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Enqueues the default frame
+ * path like aeisu_upscale_async for the geometry given here, without aeisu_configure and without
+ * allocating: the work tensor (and the FP16 policy's skip tensor) live in a static device array of
+ * 72 MiB per GPU, enough for one 1920x1080 frame in every policy (a frame that needs more is
+ * rejected with AEISU_ERR_INVALID_ARGUMENT).  Runs the runtime's current policy on its uploaded
+ * weights.  Every call on one GPU shares that array: calls that overlap on a GPU race.  Non-finite
+ * reconstructions are not reported on this path. */
+int aeisu_upscale_noalloc(aeisu_runtime* rt, int batch, int height, int width, int in_layout, int out_layout,
+                          const void* d_in, void* d_out, void* stream);
+
 /* Controller only: d_in -> packed FP16 coefficients d_meta [B][Hp/2][Wp/2][64]. */
 int aeisu_controller_async(aeisu_runtime* rt, const void* d_in, void* d_meta, void* stream);
 

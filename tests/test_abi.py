@@ -187,6 +187,7 @@ def test_argument_validation_without_device():
     assert lib.aeisu_create_sibling(None, ctypes.byref(h)) == L.AEISU_ERR_INVALID_ARGUMENT and not h.value
     assert lib.aeisu_shares_weights(None, None) == 0
     assert lib.aeisu_startup_report(None, None, 0) == 0
+    assert lib.aeisu_upscale_noalloc(None, 1, 8, 8, 0, 0, None, None, None) == L.AEISU_ERR_INVALID_ARGUMENT
 
 
 def test_header_layout_constants():
