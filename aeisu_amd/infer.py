@@ -1,40 +1,68 @@
-"""Upscale an image file or image tree on the MI355X runtime (the reference's infer.py).
+"""Command-line upscaling of an image file or a folder tree on the MI355X runtime.
 
     python -m aeisu_amd.infer --checkpoint weights/aeisu_area_mixed_fp8.bin --input lr/ --output hr/
 
-Flags and behaviour follow infer.py:9-26 of the reference: ``--tile`` is the LR core size
-(multiple of 32, 0 = whole frame), outputs are 8-bit PNGs written with round-half-up, and
-existing files are never overwritten.  ``--precision`` selects the arithmetic policy of
-the loaded artifact (default: the file's natural one).  There is no CPU path.
+Contract of the reference's CLI (infer.py:9-26): the same flags (``--tile`` is the LR core
+size, a multiple of 32, 0 for the whole frame), 8-bit PNG outputs written with round-half-up,
+and no existing file is ever replaced.  Here the whole job is planned first: every source is
+paired with its destination and every destination is checked before the first image is
+decoded, so a conflict leaves the output tree untouched.  ``--precision`` picks the
+arithmetic policy of the loaded artifact (default: the file's natural one).  All arithmetic
+runs in the HIP runtime; there is no CPU path.
 """
 from __future__ import annotations
 
 import argparse
+from dataclasses import dataclass
 from pathlib import Path
+from typing import List, Sequence
 
 from .imageio import list_images, read_rgb, save_rgb
 from .runtime import load_model, upscale
 
+PRECISIONS = ("fp16", "mixed", "mixed-fp8mma", "int8")
 
-def main(argv=None) -> None:
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--checkpoint", type=Path, required=True)
-    ap.add_argument("--input", type=Path, required=True)
-    ap.add_argument("--output", type=Path, required=True)
-    ap.add_argument("--device", default="cuda", help="HIP device, e.g. cuda or cuda:0")
-    ap.add_argument("--tile", type=int, default=128, help="LR core size, multiple of 32; zero for full frame")
-    ap.add_argument("--precision", choices=("fp16", "mixed", "mixed-fp8mma", "int8"), default=None)
-    args = ap.parse_args(argv)
-    model = load_model(args.checkpoint, args.device, args.precision)
-    images = [args.input] if args.input.is_file() else list_images(args.input)
-    if not images:
+
+@dataclass(frozen=True)
+class Job:
+    source: Path
+    destination: Path
+
+
+def plan(source: Path, output: Path) -> List[Job]:
+    """Pairs of (image, PNG to write): one file maps to ``output`` itself, a folder tree is mirrored
+    under ``output`` with every suffix replaced by .png."""
+    if source.is_file():
+        jobs = [Job(source, output)]
+    else:
+        jobs = [Job(p, output / p.relative_to(source).with_suffix(".png")) for p in list_images(source)]
+    if not jobs:
         raise ValueError("No input images found")
-    for path in images:
-        dst = args.output if args.input.is_file() else args.output / path.relative_to(args.input).with_suffix(".png")
-        if path.resolve() == dst.resolve() or dst.exists():
-            raise FileExistsError(f"Refusing to overwrite: {dst}")
-        save_rgb(dst, upscale(model, read_rgb(path), args.tile))
-        print(f"{path.name} -> {dst}", flush=True)
+    clashes = [j.destination for j in jobs if j.destination.exists() or j.destination.resolve() == j.source.resolve()]
+    if clashes:
+        raise FileExistsError(f"Refusing to overwrite: {clashes[0]}" +
+                              (f" (and {len(clashes) - 1} more)" if len(clashes) > 1 else ""))
+    return jobs
+
+
+def parse_args(argv: Sequence[str] | None) -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--checkpoint", type=Path, required=True, help="folded .pt, SPYR8F8 .bin or INT8 .pt")
+    parser.add_argument("--input", type=Path, required=True, help="an image file or a folder of images")
+    parser.add_argument("--output", type=Path, required=True, help="PNG path (file input) or folder")
+    parser.add_argument("--device", default="cuda", help="HIP device, e.g. cuda or cuda:1")
+    parser.add_argument("--tile", type=int, default=128, help="LR core size, multiple of 32; zero for full frame")
+    parser.add_argument("--precision", choices=PRECISIONS, default=None, help="arithmetic policy")
+    return parser.parse_args(argv)
+
+
+def main(argv: Sequence[str] | None = None) -> None:
+    args = parse_args(argv)
+    jobs = plan(args.input, args.output)
+    model = load_model(args.checkpoint, args.device, args.precision)
+    for n, job in enumerate(jobs, 1):
+        save_rgb(job.destination, upscale(model, read_rgb(job.source), args.tile))
+        print(f"[{n}/{len(jobs)}] {job.source.name} -> {job.destination}", flush=True)
 
 
 if __name__ == "__main__":

@@ -68,27 +68,37 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(frames_cpu, budget_s: float):
-    """FP32 oracle (reference PyTorch path restated) on whole frames until ~budget_s of work."""
+def cpu_model() -> str:
+    """CPU model name from /proc/cpuinfo (platform.processor() is empty on Linux)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.machine()
+
+
+def cpu_baseline(frames_cpu, budget_s: float, min_frames: int = 5):
+    """FP32 oracle (the reference PyTorch path restated) on whole frames: one warm-up frame, then at
+    least ``min_frames`` timed frames, more while the budget lasts (BASELINE protocol: 1 + >= 5)."""
     import torch
     from oracle import model as M
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = min(usable, int(os.environ.get("OMP_NUM_THREADS", usable)))
     torch.set_num_threads(threads)
     state = M.load_folded(ROOT / "weights" / "aeisu_area.pt")
-    f0 = frames_cpu[0].float()
-    M.upscale(state, f0[:, :256, :256], 0)                 # warm-up on a small crop
+    M.upscale(state, frames_cpu[0].float(), 0)             # warm-up: one whole frame
     done, t0 = 0, time.perf_counter()
-    while True:
+    while done < min_frames or time.perf_counter() - t0 < budget_s:
         M.upscale(state, frames_cpu[done % len(frames_cpu)].float(), 0)
         done += 1
-        if time.perf_counter() - t0 >= budget_s or done >= 8:
-            break
     elapsed = time.perf_counter() - t0
     return {"value": done / elapsed, "unit": "frames/s", "cores": threads, "kind": "port",
-            "ms_per_frame": 1000 * elapsed / done,
-            "sample": f"{done} whole {frames_cpu.shape[-2]}x{frames_cpu.shape[-1]} frame(s) through "
-                      f"oracle/model.py FP32 upscale(tile=0) (torch CPU, {threads} threads, "
-                      f"{platform.processor() or platform.machine()})"}
+            "ms_per_frame": 1000 * elapsed / done, "cpu_model": cpu_model(), "threads": threads,
+            "sample": f"1 warm-up + {done} timed whole {frames_cpu.shape[-2]}x{frames_cpu.shape[-1]} frames through "
+                      f"oracle/model.py FP32 upscale(tile=0) (torch CPU, {threads} threads on {usable} usable "
+                      f"cores, {cpu_model()})"}
 
 
 def main():

@@ -89,3 +89,26 @@ def test_paired_images(tmp_path):
     IO.save_rgb(tmp_path / "hr" / "y.jpg", torch.zeros(3, 4, 4))
     with pytest.raises(ValueError):
         IO.paired_images(tmp_path / "lr", tmp_path / "hr")
+
+
+def test_infer_plan_checks_every_destination_first(tmp_path):
+    """The CLI pairs each image with its PNG and refuses the whole job if any destination exists
+    (the reference never overwrites, infer.py:21-23), before decoding or writing anything."""
+    import numpy as np
+    from PIL import Image
+    from aeisu_amd.infer import plan
+    src = tmp_path / "in"
+    (src / "sub").mkdir(parents=True)
+    for name in ("x.jpg", "sub/y.png"):
+        Image.fromarray(np.zeros((8, 8, 3), np.uint8)).save(src / name)
+    jobs = plan(src, tmp_path / "out")
+    assert [j.destination.relative_to(tmp_path / "out").as_posix() for j in jobs] == ["sub/y.png", "x.png"]
+    assert plan(src / "x.jpg", tmp_path / "one.png")[0].destination == tmp_path / "one.png"
+    (tmp_path / "out" / "sub").mkdir(parents=True)
+    (tmp_path / "out" / "sub" / "y.png").write_bytes(b"")
+    with pytest.raises(FileExistsError, match="Refusing to overwrite"):
+        plan(src, tmp_path / "out")
+    assert not (tmp_path / "out" / "x.png").exists()
+    (tmp_path / "empty").mkdir()
+    with pytest.raises(ValueError, match="No input images found"):
+        plan(tmp_path / "empty", tmp_path / "o2")
