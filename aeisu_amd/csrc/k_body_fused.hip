@@ -151,6 +151,19 @@ __device__ __forceinline__ int ch_off(int c) { return MODE == 0 ? 2 * c : c; }
 // Raw LDS operand (E4M3 codes stay bytes until the MFMA needs them) and its MFMA form.
 template <int MODE>
 using RawOp = typename std::conditional<MODE == 3, u2, typename BodyFusedCfg<MODE>::Frag>::type;
+// LDS operand of a lane.  Byte-activation pixels are 72 bytes apart, so a 16-byte operand (INT8)
+// is only 8-byte aligned: it is read as two 8-byte halves (ds_read2_b64), since a 16-byte LDS read
+// of an address that is not 16-byte aligned runs at a fraction of the LDS rate.
+template <int MODE>
+__device__ __forceinline__ RawOp<MODE> lds_operand(const unsigned char* p) {
+  if constexpr (sizeof(RawOp<MODE>) == 16 && BodyFusedCfg<MODE>::PIX % 16 != 0) {
+    const u2* q = reinterpret_cast<const u2*>(p);
+    const u2 lo = q[0], hi = q[1];
+    return __builtin_bit_cast(RawOp<MODE>, u4{lo[0], lo[1], hi[0], hi[1]});
+  } else {
+    return *reinterpret_cast<const RawOp<MODE>*>(p);
+  }
+}
 template <int MODE>
 __device__ __forceinline__ typename BodyFusedCfg<MODE>::Frag widen(RawOp<MODE> r) {
   if constexpr (MODE == 3) return e4m3x8_to_h8(r[0], r[1]);
@@ -527,7 +540,7 @@ __device__ __forceinline__ void fb_grouped(const BodyFusedArgs& P, BodyTileF t, 
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
       const int tap = MODE == 2 ? min(2 * k + (g >> 1), 8) : k;
-      raw[k] = *reinterpret_cast<const RawOp<MODE>*>(base + ((tap / 3) * Sin + tap % 3) * C::PIX);
+      raw[k] = lds_operand<MODE>(base + ((tap / 3) * Sin + tap % 3) * C::PIX);
     }
     __builtin_amdgcn_sched_barrier(0);                 // keep the reads ahead of the MFMA chain
     Acc acc[2] = {};
@@ -561,7 +574,7 @@ __device__ __forceinline__ void expand_mma(const unsigned char* src, int qc, Fra
   RawOp<MODE> raw[NK];
 #pragma unroll
   for (int k = 0; k < NK; ++k)
-    raw[k] = *reinterpret_cast<const RawOp<MODE>*>(src + qc * C::PIX + (MODE == 2 ? 16 * g : ch_off<MODE>(32 * k + 8 * g)));
+    raw[k] = lds_operand<MODE>(src + qc * C::PIX + (MODE == 2 ? 16 * g : ch_off<MODE>(32 * k + 8 * g)));
 #pragma unroll
   for (int T = 0; T < 8; ++T) acc[T] = typename C::Acc{};
 #pragma unroll
