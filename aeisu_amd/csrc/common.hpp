@@ -96,6 +96,16 @@ __device__ __forceinline__ float leaky(float v, float slope) { return __builtin_
 // for at those stores (register dependency), before the barrier.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Next work item of a phase for this wave: the first items are dealt statically (one per wave),
+// the rest are claimed from a counter in LDS.  A SIMD issues its older waves first, so with a
+// static split the youngest waves finish last and run alone at the end of the phase; claimed
+// items let the waves that are issued more often take more, and all waves leave together.
+__device__ __forceinline__ int claim_group(int* counter, int lane) {
+  int v = 0;
+  if (lane == 0) v = atomicAdd(counter, 1);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
 // float -> OCP E4M3 with round-to-nearest-even and saturation to +-448.
 // The hardware convert rounds to nearest even but yields NaN above the
 // saturation threshold, so the value is clamped first.

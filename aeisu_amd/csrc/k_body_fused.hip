@@ -10,7 +10,7 @@
 // optimized/shader/src/int8_kernels.cuh:2-62.
 //
 // Two inputs:
-//  * BodySrc::Skip: the FP16 skip tensor written by project_kernel (per-layer-compatible path).
+//  * BodySrc::Skip (FP16 policy): the FP16 skip tensor written by project_kernel.
 //  * BodySrc::Frames16 / Frames32 (Mixed, FP8-MFMA and INT8 policies): the source frames.  The kernel
 //    recomputes the analysis features and the project 1x1 for every packed pixel the compress
 //    halo needs, feeds the project accumulators to the compress MFMA as register operands (the
@@ -123,15 +123,6 @@ __device__ __forceinline__ FragSet<MODE, N> load_frags(const void* base, int fir
 #pragma unroll
   for (int i = 0; i < N; ++i) out.f[i] = buffer_frag<F>(r, voff, (f0 + i) * 64 * (int)sizeof(F));
   return out;
-}
-
-// Next group of a phase for this wave: the first Waves groups are dealt statically (wave w
-// takes group w), the rest are claimed from a counter in LDS, so waves that the SIMD issues
-// more often take more groups and all waves leave the phase together.
-__device__ __forceinline__ int claim_group(int* counter, int lane) {
-  int v = 0;
-  if (lane == 0) v = atomicAdd(counter, 1);
-  return __builtin_amdgcn_readfirstlane(v);
 }
 
 // ---- operand and epilogue helpers ---------------------------------------------------------------
@@ -860,8 +851,6 @@ hipError_t body_fused_prepare() {
   };
   const K k[] = {
       {body_kernel_ptr<0, 0, 16>(), BodyFusedCfg<0>::Lds},     {body_kernel_ptr<0, 0, 8>(), BodyFusedCfg<0, 8>::Lds},
-      {body_kernel_ptr<1, 0, 24>(), BodyFusedCfg<1>::Lds},        {body_kernel_ptr<2, 0, 24>(), BodyFusedCfg<2>::Lds},
-      {body_kernel_ptr<3, 0, 24>(), BodyFusedCfg<3>::Lds},
       {body_kernel_ptr<1, 1, 24>(), BodyFusedCfg<1, 24>::LdsRgb}, {body_kernel_ptr<1, 2, 24>(), BodyFusedCfg<1, 24>::LdsRgb},
       {body_kernel_ptr<2, 1, 24>(), BodyFusedCfg<2, 24>::LdsRgb}, {body_kernel_ptr<2, 2, 24>(), BodyFusedCfg<2, 24>::LdsRgb},
       {body_kernel_ptr<3, 1, 24>(), BodyFusedCfg<3, 24>::LdsRgb}, {body_kernel_ptr<3, 2, 24>(), BodyFusedCfg<3, 24>::LdsRgb},
@@ -884,7 +873,6 @@ static void launch_body_t(const BodyFusedArgs& args, int tiles, hipStream_t stre
 template <int MODE>
 static void launch_body_m(BodySrc src, const BodyFusedArgs& args, int tile, int tiles, hipStream_t stream) {
   switch (src) {
-    case BodySrc::Skip: launch_body_t<MODE, 0, 24>(args, tiles, stream); break;
     case BodySrc::Frames16:
       if (tile == 16) launch_body_t<MODE, 1, 16>(args, tiles, stream);
       else launch_body_t<MODE, 1, 24>(args, tiles, stream);
@@ -909,8 +897,9 @@ hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, i
     else launch_body_t<0, 0, 8>(args, tiles, stream);
     return hipGetLastError();
   }
+  // quantized policies: frame input only (the engine runs their skip-input layers per layer)
   if (tile == 0) tile = 24;
-  if (tile != 24 && (tile != 16 || src == BodySrc::Skip)) return hipErrorInvalidValue;
+  if (src == BodySrc::Skip || (tile != 24 && tile != 16)) return hipErrorInvalidValue;
   const int tiles = body_fused_num_tiles(mode, batch, rows, args.Wl, tile);
   switch (mode) {
     case 1: launch_body_m<1>(src, args, tile, tiles, stream); break;
