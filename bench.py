@@ -47,11 +47,15 @@ KERNEL_KEYS = {"project_kernel": "project", "body_fused_kernel": "body", "fused_
                "head_kernel": "head", "refine_tail_kernel": "refine_tail"}
 
 
+PROFILE_TAGS = {1: "fp16_1080p", 2: "mixed_1080p", 3: "int8_540p_b8", 4: "mixed_1440p_b4"}
+
+
 def measured_traffic(config: int):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary (config 2 only)."""
-    path = ROOT / "profiles" / "hbm_traffic_mixed_1080p_pmc.md"
+    """HBM bytes per frame batch and stage from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of
+    the configuration (calibrated against 256 MiB device copies), keyed by stage."""
+    path = ROOT / "profiles" / f"hbm_traffic_{PROFILE_TAGS.get(config, '')}_pmc.md"
     out = {}
-    if config == 2 and path.exists():
+    if path.exists():
         for line in path.read_text().splitlines():
             if line.startswith("traffic_bytes "):
                 _, name, value = line.split()
@@ -207,7 +211,7 @@ def main():
     ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
     ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
     fused = not args.unfused                                  # fused body and fused refine+tail+head kernels
-    traffic = {} if sweep else measured_traffic(args.config)   # the profile covers config 2 as defined
+    traffic = {} if sweep else measured_traffic(args.config)   # the profiles cover configs 1-4 as defined
     kernels = {}
     proj_bytes = lr_px * 3 * s_io + packed_px * 32 * 2        # RGB in + FP16 skip out
     proj_flops = 2.0 * packed_px * 32 * 32                    # project 1x1, FP16 MFMA
@@ -231,7 +235,14 @@ def main():
                            "frac": ideal_s / bs_, "ms": stages["bottleneck"],
                            "algorithmic_flops": bflops, "hbm_gbs": body_bytes / bs_ / 1e9,
                            "algorithmic_bytes": body_bytes, "traffic": traffic.get("body"),
-                           "includes_project": body_has_project}
+                           "includes_project": body_has_project,
+                           # SQ counters (profiles/sq_counters_*): VALU issue, not the MFMA, fills the SIMD
+                           "limiter": "valu_issue"}
+        if wl["precision"] == "mixed":
+            # the reference quotes the Mixed arithmetic at the FP8 MFMA rate; this build runs its
+            # E4M3 values on the FP16 MFMA (exact products, the reference's FP32 sums)
+            fp8_ideal = ctrl_flops_low / MFMA_PEAK["fp8"] + (proj_flops / MFMA_PEAK["fp16"] if body_has_project else 0.0)
+            kernels["body"]["frac_at_fp8_peak"] = fp8_ideal / bs_
         # work in + RGB in + 2x RGB out; coefficients never leave the chip
         fused_bytes = packed_px * 32 * 2 + lr_px * (3 * s_io + 12 * s_io)
         fs = stages["head"] / 1000
@@ -240,7 +251,8 @@ def main():
             "frac": fused_bytes / fs / HBM_PEAK, "ms": stages["head"], "algorithmic_bytes": fused_bytes,
             "traffic": traffic.get("refine_tail_head"),
             "mfma_tflops": (refine_flops + synth_flops) / fs / 1e12,
-            "mfma_frac": (refine_flops + synth_flops) / fs / MFMA_PEAK["fp16"]}
+            "mfma_frac": (refine_flops + synth_flops) / fs / MFMA_PEAK["fp16"],
+            "limiter": "valu_issue"}                          # HBM is priced; VALU issue fills the SIMD
         for k in ("compress", "expand", "refine_tail") + (("project",) if body_has_project else ()):
             stages.pop(k)                                     # empty on the fused path
         # controller = project + body + the refine/tail share of the fused kernel (by MFMA count)
@@ -259,7 +271,8 @@ def main():
         ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand", "refine_tail"))
     ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK["fp16"] + ctrl_flops_low / MFMA_PEAK[low_kind]
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
-    roof = {k: v for k, v in kernels[dominant].items() if k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+    roof = {k: v for k, v in kernels[dominant].items()
+            if k in ("bound", "achieved", "peak", "unit", "frac", "traffic", "limiter")}
     roof["kernel"] = dominant
 
     if args.copy_calibration:
