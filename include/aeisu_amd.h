@@ -38,7 +38,9 @@ extern "C" {
                                    FP32 accumulation) */
 #define AEISU_PRECISION_INT8 3  /* INT8 compress/bottleneck/expand, FP16 project/refine/tail/head */
 #define AEISU_PRECISION_MIXED_FP8MMA 4 /* as MIXED, but E4M3 operands on the FP8 MFMA (higher MFMA rate,
-                                          accumulation rounded inside the unit) */
+                                          accumulation rounded inside the unit): up to 3.1/255 from the
+                                          Mixed emulation, outside the 2/255 bound of MIXED; for
+                                          comparison only */
 
 /* frame buffer layouts: planar RGB, batch-major [B][3][H][W] */
 #define AEISU_LAYOUT_NCHW_F16 0
