@@ -785,12 +785,14 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     P.px = g.px;
     const BodySrc src = g.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
     const int k = g.body_split;
-    if (k > 0) check_hip(launch_body_fused(m, src, P, k, 24, s), "fused body launch");
-    if (k < g.batch) {                             // trailing frames on 16x16 tiles
+    if (k == g.batch) {
+      check_hip(launch_body_fused(m, src, P, k, 24, s), "fused body launch");
+    } else {                                       // trailing frames on 16x16 tiles
       BodyFusedArgs Q = P;
       Q.frames = static_cast<const char*>(P.frames) + size_t(k) * 3 * g.H * g.W * (g.in_fp32 ? 4 : 2);
       Q.work = P.work + size_t(k) * g.Hq * g.Wq * 32;
-      check_hip(launch_body_fused(m, src, Q, g.batch - k, 16, s), "fused body launch");
+      if (k == 0) check_hip(launch_body_fused(m, src, Q, g.batch, 16, s), "fused body launch");
+      else check_hip(launch_body_fused_pair(m, src, P, k, 24, Q, g.batch - k, 16, s), "fused body launch");
     }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
@@ -818,14 +820,16 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     if (m != 0 || g.body_rows16 >= g.Hl) {
       check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 0, s), "fused body launch");
     } else {                                       // FP16 policy: bottom rows on 8x8 tiles
-      if (g.body_rows16 > 0) {
+      BodyFusedArgs Q = P;
+      Q.row0 = g.body_rows16;
+      Q.rows = g.Hl - g.body_rows16;
+      if (g.body_rows16 == 0) {
+        check_hip(launch_body_fused(m, BodySrc::Skip, Q, g.batch, 8, s), "fused body launch");
+      } else {
         P.row0 = 0;
         P.rows = g.body_rows16;
-        check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 16, s), "fused body launch");
+        check_hip(launch_body_fused_pair(m, BodySrc::Skip, P, g.batch, 16, Q, g.batch, 8, s), "fused body launch");
       }
-      P.row0 = g.body_rows16;
-      P.rows = g.Hl - g.body_rows16;
-      check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 8, s), "fused body launch");
     }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;

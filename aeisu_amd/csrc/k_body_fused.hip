@@ -58,6 +58,9 @@
 // issued before it, which would serialise these prefetches.  Compress prefetches the operands of its next pixel group, expand
 // issues its global loads before the MFMAs.  Blocks are mapped to tiles in XCD bands, so the
 // tiles whose compress halos overlap run in the same L2.
+#include <algorithm>
+#include <vector>
+
 #include "common.hpp"
 #include "features.hpp"
 #include "kernels.hpp"
@@ -671,18 +674,21 @@ __device__ __forceinline__ void fb_expand_rgb(const BodyFusedArgs& P, BodyTileF 
   }
 }
 
-// Block -> tile: the hardware hands blocks to the 8 XCDs round-robin (block b on XCD b % 8),
-// so XCD x runs blocks x, x + 8, ...; each XCD gets a contiguous run of tiles, and tiles whose
-// compress halos overlap share its L2.  A bijection on [0, tiles).
-__device__ __forceinline__ int body_tile_of(int b, int tiles) {
-  const int x = b & 7;
+// Block -> tile: the hardware hands blocks to the 8 XCDs round-robin (block g on XCD g % 8),
+// so each XCD gets a contiguous run of tiles, and tiles whose compress halos overlap share its L2.
+// Local block b of a launch part whose first block is `first` (global index first + b), of
+// `tiles` blocks: the part's blocks on XCD x are b = f(x), f(x) + 8, ... with f(x) = (x - first)
+// mod 8.  A bijection on [0, tiles).
+__device__ __forceinline__ int body_tile_of(int b, int tiles, int first) {
+  const int x = (first + b) & 7;
   int start = 0;
-  for (int i = 0; i < x; ++i) start += (tiles - i + 7) >> 3;
+  for (int i = 0; i < x; ++i) start += (tiles - ((i - first) & 7) + 7) >> 3;
   return start + (b >> 3);
 }
 
-template <int MODE, int SRC, int TT = BodyFusedCfg<MODE>::T>
-__global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel(BodyFusedArgs P) {
+// One output tile (tile index tidx of the launch part described by P).
+template <int MODE, int SRC, int TT>
+__device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   typedef BodyFusedCfg<MODE, TT> C;
   typedef typename std::conditional<SRC == (int)BodySrc::Frames32, float, _Float16>::type Tin;
   constexpr bool RGB = SRC != (int)BodySrc::Skip;
@@ -697,7 +703,6 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   unsigned char* slice = (C::SlicesInB ? bufB : bufB + C::SizeB + C::FragBytes) + wave * kSlice;   // frame input
   const int tx = (P.Wl + C::T - 1) / C::T, ty = ((P.rows ? P.rows : P.Hl) + C::T - 1) / C::T;
-  const int tidx = body_tile_of((int)blockIdx.x, (int)gridDim.x);
   BodyTileF t;
   t.b = tidx / (tx * ty);
   const int rem = tidx - t.b * tx * ty;
@@ -791,27 +796,57 @@ __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel
   else fb_expand<MODE, TT>(P, t, bufA, cst, Fe, wave, lane);
 }
 
+template <int MODE, int SRC, int TT = BodyFusedCfg<MODE>::T>
+__global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel(BodyFusedArgs P) {
+  body_tile<MODE, SRC, TT>(P, body_tile_of((int)blockIdx.x, (int)gridDim.x, 0));
+}
+
+// Two tile sides in one launch: blocks [0, n1) run tiles of side T1 for P1, the rest tiles of side
+// T2 for P2.  The hardware starts blocks in order as CUs free up, so the small tiles fill the CUs
+// that the last round of large tiles leaves idle, where two launches would run one after the other.
+template <int MODE, int SRC, int T1, int T2>
+__global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_pair_kernel(BodyFusedArgs P1, int n1,
+                                                                                      BodyFusedArgs P2) {
+  const int b = (int)blockIdx.x;
+  if (b < n1) body_tile<MODE, SRC, T1>(P1, body_tile_of(b, n1, 0));
+  else body_tile<MODE, SRC, T2>(P2, body_tile_of(b - n1, (int)gridDim.x - n1, n1));
+}
+
 // ------------------------------------------------------------------------------------------------
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile) {
   const int T = tile ? tile : (mode == 0 ? BodyFusedCfg<0>::T : BodyFusedCfg<3>::T);
   return batch * ((Hl + T - 1) / T) * ((Wl + T - 1) / T);
 }
 
-// Frame-input tiles: a block computes one tile, so a launch takes ceil(tiles / CUs) tile-times, and a
-// 16x16 tile costs about 0.6 of a 24x24 one (its compress region is 24^2 against 32^2 pixels, the
-// bottleneck and expand regions shrink alike).  The batch is split into leading frames on 24x24
-// tiles and trailing frames on 16x16 tiles (two launches), at the split with the fewest weighted
-// rounds: small frames at batch 1 take 16x16 tiles, 1080p and larger 24x24 ones, and a batch whose
-// 24x24 tiles leave a nearly empty last round (540p x 8) moves its last frame to 16x16 tiles.
-// Returns the number of frames on 24x24 tiles.
+// Time to run n1 blocks of cost c1 and then n2 blocks of cost c2 in one launch: the hardware hands
+// block g to XCD g % 8, and each XCD starts its next block on its first free CU (cus / 8 each).
+static double pair_makespan(long n1, double c1, long n2, double c2, int cus) {
+  const int per = cus / 8 > 0 ? cus / 8 : 1;
+  std::vector<double> busy(per);
+  double worst = 0.0;
+  for (int x = 0; x < 8; ++x) {
+    std::fill(busy.begin(), busy.end(), 0.0);
+    for (long g = x; g < n1 + n2; g += 8) *std::min_element(busy.begin(), busy.end()) += g < n1 ? c1 : c2;
+    worst = std::max(worst, *std::max_element(busy.begin(), busy.end()));
+  }
+  return worst;
+}
+
+// Frame-input tiles: a block computes one tile, and a 16x16 tile costs about 0.6 of a 24x24 one
+// (its compress region is 24^2 against 32^2 pixels, the bottleneck and expand regions shrink
+// alike).  The batch is split into leading frames on 24x24 tiles and trailing frames on 16x16
+// tiles, run in one launch (body_fused_pair_kernel), at the split with the shortest simulated
+// schedule: small frames at batch 1 take 16x16 tiles, 1080p and larger 24x24 ones, and a batch
+// whose 24x24 tiles leave a nearly empty last round (540p x 8) moves frames to 16x16 tiles, which
+// then fill the CUs of the 24x24 tiles' last round.  Returns the number of frames on 24x24 tiles.
 int body_fused_split(int mode, int batch, int Hl, int Wl, int cus) {
   if (mode == 0 || cus <= 0) return batch;
   const long t24 = body_fused_num_tiles(mode, 1, Hl, Wl, 24), t16 = body_fused_num_tiles(mode, 1, Hl, Wl, 16);
-  long best = -1;
+  double best = -1.0;
   int best_k = batch;
-  for (int k = batch; k >= 0; --k) {             // ties keep more frames on 24x24 tiles
-    const long cost = 10 * ((t24 * k + cus - 1) / cus) + 6 * ((t16 * (batch - k) + cus - 1) / cus);
-    if (best < 0 || cost < best) {
+  for (int k = batch; k >= 0; --k) {             // ties (within 1 %) keep more frames on 24x24 tiles
+    const double cost = pair_makespan(t24 * k, 1.0, t16 * (batch - k), 0.6, cus);
+    if (best < 0.0 || cost < 0.99 * best) {
       best = cost;
       best_k = k;
     }
@@ -821,19 +856,17 @@ int body_fused_split(int mode, int batch, int Hl, int Wl, int cus) {
 
 // FP16 policy: the same trade between 16x16 tiles and 8x8 tiles (compress region 16^2 against
 // 24^2 pixels plus the fixed per-tile prologue: about half the cost), split by low rows since the
-// batch is usually one frame.  1080p: 18 rows of 31 tiles (558) take three rounds of which the
-// last holds 46 tiles; rows 0-255 on 16x16 tiles (496, two rounds) and 256-279 on 8x8 tiles (183,
-// one round) take 2.5 tile-times.
+// batch is usually one frame: rows [0, R) on 16x16 tiles, the rest on 8x8 tiles, in one launch.
 int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus) {
   if (mode != 0 || cus <= 0) return Hl;
   const int top = (Hl + 15) / 16 * 16;
-  long best = -1;
+  double best = -1.0;
   int best_r = top;
-  for (int r = top; r >= 0; r -= 16) {            // ties keep more rows on 16x16 tiles
-    const long t16 = (long)batch * ((r + 15) / 16) * ((Wl + 15) / 16);
+  for (int r = top; r >= 0; r -= 16) {            // ties (within 1 %) keep more rows on 16x16 tiles
+    const long t16 = (long)batch * ((std::min(r, Hl) + 15) / 16) * ((Wl + 15) / 16);
     const long t8 = r >= Hl ? 0 : (long)batch * ((Hl - r + 7) / 8) * ((Wl + 7) / 8);
-    const long cost = 10 * ((t16 + cus - 1) / cus) + 5 * ((t8 + cus - 1) / cus);
-    if (best < 0 || cost < best) {
+    const double cost = pair_makespan(t16, 1.0, t8, 0.5, cus);
+    if (best < 0.0 || cost < 0.99 * best) {
       best = cost;
       best_r = r;
     }
@@ -843,6 +876,15 @@ int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus) {
 
 template <int MODE, int SRC, int TT>
 static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&body_fused_kernel<MODE, SRC, TT>); }
+template <int MODE, int SRC, int T1, int T2>
+static const void* body_pair_ptr() { return reinterpret_cast<const void*>(&body_fused_pair_kernel<MODE, SRC, T1, T2>); }
+// dynamic LDS of a launch of tile side TT
+template <int MODE, int SRC, int TT>
+constexpr int body_lds() { return SRC ? BodyFusedCfg<MODE, TT>::LdsRgb : BodyFusedCfg<MODE, TT>::Lds; }
+template <int MODE, int SRC, int T1, int T2>
+constexpr int body_pair_lds() {
+  return body_lds<MODE, SRC, T1>() > body_lds<MODE, SRC, T2>() ? body_lds<MODE, SRC, T1>() : body_lds<MODE, SRC, T2>();
+}
 
 hipError_t body_fused_prepare() {
   struct K {
@@ -856,7 +898,11 @@ hipError_t body_fused_prepare() {
       {body_kernel_ptr<3, 1, 24>(), BodyFusedCfg<3, 24>::LdsRgb}, {body_kernel_ptr<3, 2, 24>(), BodyFusedCfg<3, 24>::LdsRgb},
       {body_kernel_ptr<1, 1, 16>(), BodyFusedCfg<1, 16>::LdsRgb}, {body_kernel_ptr<1, 2, 16>(), BodyFusedCfg<1, 16>::LdsRgb},
       {body_kernel_ptr<2, 1, 16>(), BodyFusedCfg<2, 16>::LdsRgb}, {body_kernel_ptr<2, 2, 16>(), BodyFusedCfg<2, 16>::LdsRgb},
-      {body_kernel_ptr<3, 1, 16>(), BodyFusedCfg<3, 16>::LdsRgb}, {body_kernel_ptr<3, 2, 16>(), BodyFusedCfg<3, 16>::LdsRgb}};
+      {body_kernel_ptr<3, 1, 16>(), BodyFusedCfg<3, 16>::LdsRgb}, {body_kernel_ptr<3, 2, 16>(), BodyFusedCfg<3, 16>::LdsRgb},
+      {body_pair_ptr<0, 0, 16, 8>(), body_pair_lds<0, 0, 16, 8>()},
+      {body_pair_ptr<1, 1, 24, 16>(), body_pair_lds<1, 1, 24, 16>()}, {body_pair_ptr<1, 2, 24, 16>(), body_pair_lds<1, 2, 24, 16>()},
+      {body_pair_ptr<2, 1, 24, 16>(), body_pair_lds<2, 1, 24, 16>()}, {body_pair_ptr<2, 2, 24, 16>(), body_pair_lds<2, 2, 24, 16>()},
+      {body_pair_ptr<3, 1, 24, 16>(), body_pair_lds<3, 1, 24, 16>()}, {body_pair_ptr<3, 2, 24, 16>(), body_pair_lds<3, 2, 24, 16>()}};
   for (const K& e : k) {
     const hipError_t r = hipFuncSetAttribute(e.fn, hipFuncAttributeMaxDynamicSharedMemorySize, e.lds);
     if (r != hipSuccess) return r;
@@ -905,6 +951,44 @@ hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, i
     case 1: launch_body_m<1>(src, args, tile, tiles, stream); break;
     case 2: launch_body_m<2>(src, args, tile, tiles, stream); break;
     default: launch_body_m<3>(src, args, tile, tiles, stream); break;
+  }
+  return hipGetLastError();
+}
+
+template <int MODE, int SRC, int T1, int T2>
+static void launch_pair_t(const BodyFusedArgs& a1, int n1, const BodyFusedArgs& a2, int n2, hipStream_t stream) {
+  constexpr int lds = body_pair_lds<MODE, SRC, T1, T2>();
+  hipLaunchKernelGGL((body_fused_pair_kernel<MODE, SRC, T1, T2>), dim3(n1 + n2), dim3(BodyFusedCfg<MODE>::Threads),
+                     lds, stream, a1, n1, a2);
+}
+template <int MODE>
+static void launch_pair_m(BodySrc src, const BodyFusedArgs& a1, int n1, const BodyFusedArgs& a2, int n2,
+                          hipStream_t stream) {
+  if (src == BodySrc::Frames16) launch_pair_t<MODE, 1, 24, 16>(a1, n1, a2, n2, stream);
+  else launch_pair_t<MODE, 2, 24, 16>(a1, n1, a2, n2, stream);
+}
+
+hipError_t launch_body_fused_pair(int mode, BodySrc src, const BodyFusedArgs& a1, int batch1, int tile1,
+                                  const BodyFusedArgs& a2, int batch2, int tile2, hipStream_t stream) {
+  for (const BodyFusedArgs* a : {&a1, &a2}) {
+    const int rows = a->rows ? a->rows : a->Hl;
+    if (a->row0 < 0 || rows < 1 || a->row0 + rows > a->Hl) return hipErrorInvalidValue;
+  }
+  if (batch1 < 1 || batch2 < 1) return hipErrorInvalidValue;
+  if (mode == 0) {
+    if (src != BodySrc::Skip || tile1 != 16 || tile2 != 8) return hipErrorInvalidValue;
+    const int n1 = body_fused_num_tiles(0, batch1, a1.rows ? a1.rows : a1.Hl, a1.Wl, 16);
+    const int n2 = body_fused_num_tiles(0, batch2, a2.rows ? a2.rows : a2.Hl, a2.Wl, 8);
+    launch_pair_t<0, 0, 16, 8>(a1, n1, a2, n2, stream);
+    return hipGetLastError();
+  }
+  if (src == BodySrc::Skip || tile1 != 24 || tile2 != 16) return hipErrorInvalidValue;
+  const int n1 = body_fused_num_tiles(mode, batch1, a1.rows ? a1.rows : a1.Hl, a1.Wl, 24);
+  const int n2 = body_fused_num_tiles(mode, batch2, a2.rows ? a2.rows : a2.Hl, a2.Wl, 16);
+  switch (mode) {
+    case 1: launch_pair_m<1>(src, a1, n1, a2, n2, stream); break;
+    case 2: launch_pair_m<2>(src, a1, n1, a2, n2, stream); break;
+    default: launch_pair_m<3>(src, a1, n1, a2, n2, stream); break;
   }
   return hipGetLastError();
 }

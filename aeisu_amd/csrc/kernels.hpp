@@ -65,6 +65,10 @@ int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();
 hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
                              hipStream_t stream);
+// two parts in one launch: batch1 frames (or a1's rows) on tile1 tiles, then batch2 frames (a2's
+// rows) on tile2 tiles; tiles (24, 16) for the quantized policies, (16, 8) for the FP16 policy
+hipError_t launch_body_fused_pair(int mode, BodySrc src, const BodyFusedArgs& a1, int batch1, int tile1,
+                                  const BodyFusedArgs& a2, int batch2, int tile2, hipStream_t stream);
 
 // Fused refine + tail + head (coefficients in LDS); one block per CU (1024 threads for FP16
 // frames, 768 for FP32 frames).
