@@ -342,6 +342,7 @@ struct Geometry {
                                    // no skip tensor); the quantized policies
   int nlow = 0;                    // body activations in device memory (per-layer path)
   int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
+  int body_cols24 = 0;             // frame-input body: > 0: low columns [0, body_cols24) on 24x24 tiles, the rest on 16x16
   int body_rows16 = 0;             // FP16 policy body: low rows on 16x16 tiles, the rest on 8x8
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
 
@@ -744,7 +745,9 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
   g.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, mode), cus);
   g.grid.refine = clamp_grid(refine_num_tiles(batch, g.Hq, g.Wq), refine_blocks_per_cu(), cus);
   g.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(g.in_fp32, g.out_fp32), cus);
-  g.body_split = (flags & AEISU_FLAG_BODY_TILE24) ? batch : body_fused_split(mode, batch, g.Hl, g.Wl, cus);
+  const BodyPlan plan = (flags & AEISU_FLAG_BODY_TILE24) ? BodyPlan{batch, 0} : body_fused_plan(mode, batch, g.Hl, g.Wl, cus);
+  g.body_split = plan.frames24;
+  g.body_cols24 = plan.cols24;
   g.body_rows16 = (flags & AEISU_FLAG_BODY_TILE24) ? g.Hl : body_fused_row_split(mode, batch, g.Hl, g.Wl, cus);
   g.grid.fused = clamp_grid(fused_num_tiles(g.in_fp32, batch, height, width, g.Hq, g.Wq, g.py, g.px), 1, cus);
   return g;
@@ -785,7 +788,14 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     P.px = g.px;
     const BodySrc src = g.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
     const int k = g.body_split;
-    if (k == g.batch) {
+    if (g.body_cols24 > 0) {                       // right-hand columns on 16x16 tiles
+      BodyFusedArgs Q = P;
+      P.col0 = 0;
+      P.cols = g.body_cols24;
+      Q.col0 = g.body_cols24;
+      Q.cols = g.Wl - g.body_cols24;
+      check_hip(launch_body_fused_pair(m, src, P, g.batch, 24, Q, g.batch, 16, s), "fused body launch");
+    } else if (k == g.batch) {
       check_hip(launch_body_fused(m, src, P, k, 24, s), "fused body launch");
     } else {                                       // trailing frames on 16x16 tiles
       BodyFusedArgs Q = P;
@@ -897,7 +907,7 @@ static std::string startup_report(const Runtime& rt) {
     << " source=" << g.W << 'x' << g.H << " batch=" << g.batch << " padded=" << g.Wp << 'x' << g.Hp
     << " packed=" << g.Wq << 'x' << g.Hq << " low=" << g.Wl << 'x' << g.Hl << " source_pad=" << g.px << ','
     << g.py << " io=" << (g.in_fp32 ? "f32" : "f16") << '/' << (g.out_fp32 ? "f32" : "f16")
-    << " body_tiles24_frames=" << g.body_split << " weights_bytes=" << rt.w->bytes()
+    << " body_tiles24_frames=" << g.body_split << " body_tiles24_cols=" << g.body_cols24 << " weights_bytes=" << rt.w->bytes()
     << " scratch_bytes=" << rt.scratch_bytes() << " shared_model_users=" << rt.model.use_count();
   return r.str();
 }

@@ -34,8 +34,8 @@
 //  * byte activations (E4M3 codes, INT8): T = 24 (252 tiles at 1080p, one per CU), 72 bytes
 //    per LDS pixel; the Mixed policy widens codes to FP16 operands with
 //    v_cvt_scalef32_pk_f16_fp8 as it reads them.  The frame-input variants also come with
-//    T = 16 for frames whose 24x24 tiles would leave CUs idle (body_fused_split picks the
-//    tile per batch, possibly two launches: leading frames on 24x24, trailing on 16x16 tiles).
+//    T = 16 for frames whose 24x24 tiles would leave CUs idle (body_fused_plan picks the tiles
+//    per shape: trailing frames or right-hand columns on 16x16 tiles, in the same launch).
 //  * FP16 activations: T = 16, 144 bytes per LDS pixel.
 // 12 waves (3 per SIMD, up to 168 VGPRs each): compress and expand split the pixel groups over
 // all waves; in a grouped layer, wave w serves group w & 1 and keeps that group's 18 weight
@@ -702,12 +702,12 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   unsigned char* bufB = bufA + C::SizeA;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   unsigned char* slice = (C::SlicesInB ? bufB : bufB + C::SizeB + C::FragBytes) + wave * kSlice;   // frame input
-  const int tx = (P.Wl + C::T - 1) / C::T, ty = ((P.rows ? P.rows : P.Hl) + C::T - 1) / C::T;
+  const int tx = ((P.cols ? P.cols : P.Wl) + C::T - 1) / C::T, ty = ((P.rows ? P.rows : P.Hl) + C::T - 1) / C::T;
   BodyTileF t;
   t.b = tidx / (tx * ty);
   const int rem = tidx - t.b * tx * ty;
   t.y0 = P.row0 + (rem / tx) * C::T;
-  t.x0 = (rem % tx) * C::T;
+  t.x0 = P.col0 + (rem % tx) * C::T;
   // constants, compress weights and the first group's operands are in flight together
   float cv[CPT];
 #pragma unroll
@@ -834,24 +834,36 @@ static double pair_makespan(long n1, double c1, long n2, double c2, int cus) {
 
 // Frame-input tiles: a block computes one tile, and a 16x16 tile costs about 0.6 of a 24x24 one
 // (its compress region is 24^2 against 32^2 pixels, the bottleneck and expand regions shrink
-// alike).  The batch is split into leading frames on 24x24 tiles and trailing frames on 16x16
-// tiles, run in one launch (body_fused_pair_kernel), at the split with the shortest simulated
-// schedule: small frames at batch 1 take 16x16 tiles, 1080p and larger 24x24 ones, and a batch
-// whose 24x24 tiles leave a nearly empty last round (540p x 8) moves frames to 16x16 tiles, which
-// then fill the CUs of the 24x24 tiles' last round.  Returns the number of frames on 24x24 tiles.
-int body_fused_split(int mode, int batch, int Hl, int Wl, int cus) {
-  if (mode == 0 || cus <= 0) return batch;
+// alike).  Two tile sides run in one launch (body_fused_pair_kernel), and the plan with the
+// shortest simulated schedule is taken (ties, within 1 %, keep more 24x24 tiles):
+//  * frames: the leading frames on 24x24 tiles, the rest on 16x16 tiles.  Small frames at batch 1
+//    take 16x16 tiles, 1080p and larger 24x24 ones.
+//  * columns: every frame's low columns [0, C) on 24x24 tiles (C a multiple of 24), the rest on
+//    16x16 tiles.  Where a frame's last 24-wide tile column is mostly past the frame (540p: 248
+//    low columns, 8 in the eleventh tile column), 16x16 tiles cover it for less, and a batch that
+//    needed a third round of 24x24 tiles (540p x 8: 528 tiles on 256 CUs) fits in about two.
+BodyPlan body_fused_plan(int mode, int batch, int Hl, int Wl, int cus) {
+  BodyPlan best_plan{batch, 0};
+  if (mode == 0 || cus <= 0) return best_plan;
   const long t24 = body_fused_num_tiles(mode, 1, Hl, Wl, 24), t16 = body_fused_num_tiles(mode, 1, Hl, Wl, 16);
   double best = -1.0;
-  int best_k = batch;
-  for (int k = batch; k >= 0; --k) {             // ties (within 1 %) keep more frames on 24x24 tiles
+  for (int k = batch; k >= 0; --k) {
     const double cost = pair_makespan(t24 * k, 1.0, t16 * (batch - k), 0.6, cus);
     if (best < 0.0 || cost < 0.99 * best) {
       best = cost;
-      best_k = k;
+      best_plan = BodyPlan{k, 0};
     }
   }
-  return best_k;
+  for (int c = (Wl - 1) / 24 * 24; c >= 24; c -= 24) {
+    const long n24 = (long)batch * body_fused_num_tiles(mode, 1, Hl, c, 24);
+    const long n16 = (long)batch * body_fused_num_tiles(mode, 1, Hl, Wl - c, 16);
+    const double cost = pair_makespan(n24, 1.0, n16, 0.6, cus);
+    if (cost < 0.99 * best) {
+      best = cost;
+      best_plan = BodyPlan{batch, c};
+    }
+  }
+  return best_plan;
 }
 
 // FP16 policy: the same trade between 16x16 tiles and 8x8 tiles (compress region 16^2 against
@@ -932,13 +944,14 @@ static void launch_body_m(BodySrc src, const BodyFusedArgs& args, int tile, int 
 
 hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
                              hipStream_t stream) {
-  const int rows = args.rows ? args.rows : args.Hl;
+  const int rows = args.rows ? args.rows : args.Hl, cols = args.cols ? args.cols : args.Wl;
   if (args.row0 < 0 || rows < 1 || args.row0 + rows > args.Hl) return hipErrorInvalidValue;
+  if (args.col0 < 0 || cols < 1 || args.col0 + cols > args.Wl) return hipErrorInvalidValue;
   if (mode == 0) {
     // FP16 policy: skip input only (its FP16 hi/lo project operands need twice the feature slice)
     if (tile == 0) tile = 16;
     if (src != BodySrc::Skip || (tile != 16 && tile != 8)) return hipErrorInvalidValue;
-    const int tiles = body_fused_num_tiles(0, batch, rows, args.Wl, tile);
+    const int tiles = body_fused_num_tiles(0, batch, rows, cols, tile);
     if (tile == 16) launch_body_t<0, 0, 16>(args, tiles, stream);
     else launch_body_t<0, 0, 8>(args, tiles, stream);
     return hipGetLastError();
@@ -946,7 +959,7 @@ hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, i
   // quantized policies: frame input only (the engine runs their skip-input layers per layer)
   if (tile == 0) tile = 24;
   if (src == BodySrc::Skip || (tile != 24 && tile != 16)) return hipErrorInvalidValue;
-  const int tiles = body_fused_num_tiles(mode, batch, rows, args.Wl, tile);
+  const int tiles = body_fused_num_tiles(mode, batch, rows, cols, tile);
   switch (mode) {
     case 1: launch_body_m<1>(src, args, tile, tiles, stream); break;
     case 2: launch_body_m<2>(src, args, tile, tiles, stream); break;
@@ -971,20 +984,23 @@ static void launch_pair_m(BodySrc src, const BodyFusedArgs& a1, int n1, const Bo
 hipError_t launch_body_fused_pair(int mode, BodySrc src, const BodyFusedArgs& a1, int batch1, int tile1,
                                   const BodyFusedArgs& a2, int batch2, int tile2, hipStream_t stream) {
   for (const BodyFusedArgs* a : {&a1, &a2}) {
-    const int rows = a->rows ? a->rows : a->Hl;
+    const int rows = a->rows ? a->rows : a->Hl, cols = a->cols ? a->cols : a->Wl;
     if (a->row0 < 0 || rows < 1 || a->row0 + rows > a->Hl) return hipErrorInvalidValue;
+    if (a->col0 < 0 || cols < 1 || a->col0 + cols > a->Wl) return hipErrorInvalidValue;
   }
+  auto rows_of = [](const BodyFusedArgs& a) { return a.rows ? a.rows : a.Hl; };
+  auto cols_of = [](const BodyFusedArgs& a) { return a.cols ? a.cols : a.Wl; };
   if (batch1 < 1 || batch2 < 1) return hipErrorInvalidValue;
   if (mode == 0) {
     if (src != BodySrc::Skip || tile1 != 16 || tile2 != 8) return hipErrorInvalidValue;
-    const int n1 = body_fused_num_tiles(0, batch1, a1.rows ? a1.rows : a1.Hl, a1.Wl, 16);
-    const int n2 = body_fused_num_tiles(0, batch2, a2.rows ? a2.rows : a2.Hl, a2.Wl, 8);
+    const int n1 = body_fused_num_tiles(0, batch1, rows_of(a1), cols_of(a1), 16);
+    const int n2 = body_fused_num_tiles(0, batch2, rows_of(a2), cols_of(a2), 8);
     launch_pair_t<0, 0, 16, 8>(a1, n1, a2, n2, stream);
     return hipGetLastError();
   }
   if (src == BodySrc::Skip || tile1 != 24 || tile2 != 16) return hipErrorInvalidValue;
-  const int n1 = body_fused_num_tiles(mode, batch1, a1.rows ? a1.rows : a1.Hl, a1.Wl, 24);
-  const int n2 = body_fused_num_tiles(mode, batch2, a2.rows ? a2.rows : a2.Hl, a2.Wl, 16);
+  const int n1 = body_fused_num_tiles(mode, batch1, rows_of(a1), cols_of(a1), 24);
+  const int n2 = body_fused_num_tiles(mode, batch2, rows_of(a2), cols_of(a2), 16);
   switch (mode) {
     case 1: launch_pair_m<1>(src, a1, n1, a2, n2, stream); break;
     case 2: launch_pair_m<2>(src, a1, n1, a2, n2, stream); break;

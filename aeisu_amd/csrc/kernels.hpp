@@ -54,12 +54,17 @@ struct BodyFusedArgs {
   int Hl, Wl;
   int H, W, py, px;        // frame geometry (frame-input variants)
   int row0, rows;          // low-grid rows this launch covers: [row0, row0 + rows); rows = 0: all
+  int col0, cols;          // low-grid columns likewise: [col0, col0 + cols); cols = 0: all
 };
 // tile = side of the body's output tile in low pixels (0: the policy's default, 24, or 16 for the FP16 policy)
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile = 0);
-// frame-input body: how many leading frames of a batch run on 24x24 tiles (the rest on 16x16 tiles)
-// on a device with `cus` compute units
-int body_fused_split(int mode, int batch, int Hl, int Wl, int cus);
+// Frame-input body plan on a device with `cus` compute units: the leading `frames24` frames on 24x24
+// tiles and the rest on 16x16 tiles, or (cols24 > 0) every frame's low columns [0, cols24) on 24x24
+// tiles and the rest on 16x16 tiles
+struct BodyPlan {
+  int frames24, cols24;
+};
+BodyPlan body_fused_plan(int mode, int batch, int Hl, int Wl, int cus);
 // FP16 policy (skip input): low rows [0, R) on 16x16 tiles, the rest on 8x8 tiles; returns R
 int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();
