@@ -344,6 +344,8 @@ struct Geometry {
   int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
   int body_cols24 = 0;             // frame-input body: > 0: low columns [0, body_cols24) on 24x24 tiles, the rest on 16x16
   int body_rows16 = 0;             // FP16 policy body: low rows on 16x16 tiles, the rest on 8x8
+  int body_xc_tile = 0;            // frame-input body with the compress exchange: its tile side (0: off)
+  int cus = 0;                     // compute units of the device
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
 
   size_t packed() const { return size_t(batch) * Hq * Wq; }
@@ -352,6 +354,11 @@ struct Geometry {
   size_t skip_bytes() const { return fused_rgb ? 0 : packed() * 32 * 2; }
   size_t work_bytes() const { return packed() * 32 * 2; }
   size_t meta_bytes() const { return fused ? 0 : packed() * 64 * 2; }
+  // compress exchange: the cores' compress codes (64 bytes per low pixel) and one counter per tile
+  size_t xbuf_bytes() const { return body_xc_tile ? lowpx() * 64 : 0; }
+  size_t xflag_bytes() const {
+    return body_xc_tile ? size_t(body_fused_num_tiles(2, batch, Hl, Wl, body_xc_tile)) * sizeof(int) : 0;
+  }
 };
 
 // Device pointers the kernels of one frame use beyond the inputs, outputs and weights.
@@ -360,7 +367,9 @@ struct Scratch {
   void* work = nullptr;
   void* meta = nullptr;
   void* low[5] = {};
-  unsigned* nonfinite = nullptr;
+  unsigned* nonfinite = nullptr;   // [0] non-finite output, [1] compress-exchange wait ran out
+  void* xbuf = nullptr;
+  int* xflags = nullptr;
 };
 
 struct Runtime {
@@ -369,7 +378,7 @@ struct Runtime {
   const ModeWeights* w = nullptr;  // the policy this runtime runs
   bool configured = false;
   Geometry g;
-  DeviceBuffer skip, work, meta, nonfinite;
+  DeviceBuffer skip, work, meta, nonfinite, xbuf, xflags;
   DeviceBuffer low[5];
   std::string report;              // startup report of the configuration
   // captured frame graphs, one per (input, output) buffer pair
@@ -406,10 +415,12 @@ struct Runtime {
     sc.meta = meta.ptr;
     for (int i = 0; i < 5; ++i) sc.low[i] = low[i].ptr;
     sc.nonfinite = nonfinite.as<unsigned>();
+    sc.xbuf = xbuf.ptr;
+    sc.xflags = xflags.as<int>();
     return sc;
   }
   size_t scratch_bytes() const {
-    size_t n = skip.bytes + work.bytes + meta.bytes + nonfinite.bytes;
+    size_t n = skip.bytes + work.bytes + meta.bytes + nonfinite.bytes + xbuf.bytes + xflags.bytes;
     for (const auto& l : low) n += l.bytes;
     return n;
   }
@@ -704,7 +715,7 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
       (out_layout != AEISU_LAYOUT_NCHW_F16 && out_layout != AEISU_LAYOUT_NCHW_F32))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unsupported frame layout");
   if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD | AEISU_FLAG_UNFUSED |
-                AEISU_FLAG_BODY_TILE24))
+                AEISU_FLAG_BODY_TILE24 | AEISU_FLAG_BODY_NO_EXCHANGE))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unknown configure flag");
   const bool no_pad = flags & AEISU_FLAG_NO_PAD;
   if (no_pad && (height % 4 || width % 4))
@@ -749,6 +760,14 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
   g.body_split = plan.frames24;
   g.body_cols24 = plan.cols24;
   g.body_rows16 = (flags & AEISU_FLAG_BODY_TILE24) ? g.Hl : body_fused_row_split(mode, batch, g.Hl, g.Wl, cus);
+  g.cus = cus;
+  // compress exchange: a whole-frame launch of one tile side whose tiles all fit on the device at once
+  // (one block per CU)
+  if (g.fused_rgb && !(flags & AEISU_FLAG_BODY_NO_EXCHANGE) && plan.cols24 == 0 &&
+      (plan.frames24 == batch || plan.frames24 == 0)) {
+    const int tile = plan.frames24 == batch ? 24 : 16;
+    if (body_fused_num_tiles(mode, batch, g.Hl, g.Wl, tile) <= cus) g.body_xc_tile = tile;
+  }
   g.grid.fused = clamp_grid(fused_num_tiles(g.in_fp32, batch, height, width, g.Hq, g.Wq, g.py, g.px), 1, cus);
   return g;
 }
@@ -788,7 +807,12 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     P.px = g.px;
     const BodySrc src = g.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
     const int k = g.body_split;
-    if (g.body_cols24 > 0) {                       // right-hand columns on 16x16 tiles
+    if (g.body_xc_tile) {                          // compress exchange between neighbouring tiles
+      P.xbuf = static_cast<unsigned char*>(sc.xbuf);
+      P.xflags = sc.xflags;
+      P.xerr = sc.nonfinite + 1;
+      check_hip(launch_body_fused_xc(m, src, P, g.batch, g.body_xc_tile, g.cus, s), "fused body launch");
+    } else if (g.body_cols24 > 0) {                       // right-hand columns on 16x16 tiles
       BodyFusedArgs Q = P;
       P.col0 = 0;
       P.cols = g.body_cols24;
@@ -907,7 +931,8 @@ static std::string startup_report(const Runtime& rt) {
     << " source=" << g.W << 'x' << g.H << " batch=" << g.batch << " padded=" << g.Wp << 'x' << g.Hp
     << " packed=" << g.Wq << 'x' << g.Hq << " low=" << g.Wl << 'x' << g.Hl << " source_pad=" << g.px << ','
     << g.py << " io=" << (g.in_fp32 ? "f32" : "f16") << '/' << (g.out_fp32 ? "f32" : "f16")
-    << " body_tiles24_frames=" << g.body_split << " body_tiles24_cols=" << g.body_cols24 << " weights_bytes=" << rt.w->bytes()
+    << " body_tiles24_frames=" << g.body_split << " body_tiles24_cols=" << g.body_cols24
+    << " body_exchange_tile=" << g.body_xc_tile << " weights_bytes=" << rt.w->bytes()
     << " scratch_bytes=" << rt.scratch_bytes() << " shared_model_users=" << rt.model.use_count();
   return r.str();
 }
@@ -925,8 +950,11 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.work.alloc(g.work_bytes());
   rt.meta.alloc(g.meta_bytes());
   for (int i = 0; i < 5; ++i) rt.low[i].alloc(i < g.nlow ? g.lowpx() * 64 * (mode == 0 ? 2 : 1) : 0);
-  rt.nonfinite.alloc(4);
-  check_hip(hipMemset(rt.nonfinite.ptr, 0, 4), "hipMemset(flag)");
+  rt.nonfinite.alloc(8);
+  check_hip(hipMemset(rt.nonfinite.ptr, 0, 8), "hipMemset(flags)");
+  rt.xbuf.alloc(g.xbuf_bytes());
+  rt.xflags.alloc(g.xflag_bytes());
+  if (rt.xflags.ptr) check_hip(hipMemset(rt.xflags.ptr, 0, rt.xflags.bytes), "hipMemset(exchange counters)");
   if (precision) rt.precision = precision;
   rt.mode = mode;
   rt.w = &w;
@@ -955,8 +983,9 @@ static void require_configured(const Runtime& rt) {
 // each 256-byte aligned.
 static void enqueue_noalloc(const Runtime& rt, int batch, int height, int width, int in_layout, int out_layout,
                             const void* d_in, void* d_out, hipStream_t s) {
-  const Geometry g = make_geometry(rt.mode, rt.w->project_precise, rt.model->cu_count, batch, height, width,
-                                   in_layout, out_layout, 0);
+  Geometry g = make_geometry(rt.mode, rt.w->project_precise, rt.model->cu_count, batch, height, width, in_layout,
+                             out_layout, 0);
+  g.body_xc_tile = 0;                              // the exchange needs its own zeroed counters
   auto up = [](size_t n) { return (n + 255) & ~size_t(255); };
   const size_t need = 256 + up(g.skip_bytes()) + up(g.work_bytes());
   if (need > kNoAllocScratchBytes)
@@ -1118,17 +1147,20 @@ int aeisu_check_finite(aeisu_runtime* h, void* stream) {
   const int rc = guarded([&] {
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
-    unsigned flag = 0;
-    aeisu::check_hip(hipMemcpyAsync(&flag, rt.nonfinite.ptr, 4, hipMemcpyDeviceToHost, (hipStream_t)stream), "flag readback");
+    unsigned flag[2] = {0u, 0u};
+    aeisu::check_hip(hipMemcpyAsync(flag, rt.nonfinite.ptr, 8, hipMemcpyDeviceToHost, (hipStream_t)stream), "flag readback");
     aeisu::check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
-    if (flag) {
-      aeisu::check_hip(hipMemsetAsync(rt.nonfinite.ptr, 0, 4, (hipStream_t)stream), "flag reset");
+    if (flag[0] || flag[1]) {
+      aeisu::check_hip(hipMemsetAsync(rt.nonfinite.ptr, 0, 8, (hipStream_t)stream), "flag reset");
       aeisu::check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
-      status = AEISU_ERR_NONFINITE;
+      status = flag[1] ? AEISU_ERR_HIP : AEISU_ERR_NONFINITE;
     }
   });
   if (rc != AEISU_OK) return rc;
-  if (status != AEISU_OK) g_last_error = "Non-finite model reconstruction";
+  if (status == AEISU_ERR_HIP)
+    g_last_error = "fused body: a tile's wait for its neighbours' compress ran out (the frame is invalid)";
+  else if (status != AEISU_OK)
+    g_last_error = "Non-finite model reconstruction";
   return status;
 }
 

@@ -37,6 +37,11 @@
 //    T = 16 for frames whose 24x24 tiles would leave CUs idle (body_fused_plan picks the tiles
 //    per shape: trailing frames or right-hand columns on 16x16 tiles, in the same launch).
 //  * FP16 activations: T = 16, 144 bytes per LDS pixel.
+// Compress exchange (body_fused_xc_kernel, frame input): when a whole-frame launch has no more tiles
+// than the device has CUs, every tile is resident at once, so a tile computes compress on its T x T
+// core only and takes the 4-pixel ring of R0 from its neighbours' cores through a device-memory
+// tensor (exchange_publish / exchange_collect): the compress work per tile drops from (T+8)^2 to
+// T^2 pixels (1080p: 64 to 36 pixel groups).  The codes are the same, so the result is too.
 // 12 waves (3 per SIMD, up to 168 VGPRs each): compress and expand split the pixel groups over
 // all waves; in a grouped layer, wave w serves group w & 1 and keeps that group's 18 weight
 // fragments in registers for the layer.
@@ -67,7 +72,8 @@
 
 namespace aeisu {
 
-constexpr int kBodySliceBytes = 64 * 40 * 2;      // a wave's RGB stage / feature slice (frame input)
+constexpr int kBodySliceBytes = 64 * 40 * 2;
+constexpr int kLoadDeviceScope = 16;               // buffer-load cache policy: sc1 (device scope)      // a wave's RGB stage / feature slice (frame input)
 
 template <int MODE, int TT = (MODE == 0 ? 16 : 24)>
 struct BodyFusedCfg {
@@ -175,6 +181,19 @@ __device__ __forceinline__ float act_value(typename BodyFusedCfg<MODE>::Acc acc,
   else if constexpr (MODE == 1 || MODE == 3) return leaky(fmaf(acc[r], sc, bs), 0.1f) * inv_out;
   else return __builtin_rintf(leaky(fmaf((float)acc[r], sc, bs), 0.1f) * inv_out);
 }
+// Byte codes of 4 consecutive channels (E4M3 saturating RNE, or INT8 clamped to +-127).
+template <int MODE>
+__device__ __forceinline__ unsigned pack_codes4(const float (&v)[4]) {
+  static_assert(MODE != 0, "byte-activation policies");
+  if constexpr (MODE == 1 || MODE == 3) {
+    return pack_e4m3x4(v[0], v[1], v[2], v[3]);
+  } else {
+    int q[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) q[r] = (int)__builtin_amdgcn_fmed3f(v[r], -127.0f, 127.0f);
+    return pack_s8x4(q[0], q[1], q[2], q[3]);
+  }
+}
 template <int MODE>
 __device__ __forceinline__ void pack_store(unsigned char* dst, const float (&v)[4], bool inside) {
   if constexpr (MODE == 0) {
@@ -183,14 +202,8 @@ __device__ __forceinline__ void pack_store(unsigned char* dst, const float (&v)[
     w[1] = pack_h2(v[2], v[3]);
     if (!inside) w = u2{0u, 0u};
     *reinterpret_cast<u2*>(dst) = w;
-  } else if constexpr (MODE == 1 || MODE == 3) {
-    const unsigned w = pack_e4m3x4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<unsigned*>(dst) = inside ? w : 0u;
   } else {
-    int q[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) q[r] = (int)__builtin_amdgcn_fmed3f(v[r], -127.0f, 127.0f);
-    const unsigned w = pack_s8x4(q[0], q[1], q[2], q[3]);
+    const unsigned w = pack_codes4<MODE>(v);
     *reinterpret_cast<unsigned*>(dst) = inside ? w : 0u;
   }
 }
@@ -292,6 +305,38 @@ __device__ __forceinline__ void compress_store(const BodyFusedArgs& P, BodyTileF
       store_act4<MODE>(dst + q * C::PIX + ch_off<MODE>(c0), acc[T], *reinterpret_cast<const f4*>(cst + kCstCompress + c0),
                        *reinterpret_cast<const f4*>(cst + kCstCompress + 64 + c0), P.inv_out[0], inside);
     }
+  }
+}
+
+// Compress epilogue of group pg of the T x T tile core (compress exchange): into its place in
+// region R0 and, for the pixels within 4 of the core's edge that lie in the low grid, into the
+// exchange tensor, from which the neighbouring tiles take their ring of R0.
+template <int MODE, int TT>
+__device__ __forceinline__ void compress_store_core(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst,
+                                                    const float* cst, const typename BodyFusedCfg<MODE>::Acc (&acc)[4],
+                                                    int pg, int lane) {
+  typedef BodyFusedCfg<MODE, TT> C;
+  static_assert((C::T * C::T) % 16 == 0, "core groups cover whole tiles");
+  const int n = lane & 15, g = lane >> 4;
+  const int q = pg * 16 + n;
+  const int r = q / C::T, c = q - r * C::T;
+  const int gy = t.y0 + r, gx = t.x0 + c;
+  const bool inside = (gy < P.Hl) & (gx < P.Wl);
+  const bool border = (r < 4) | (r >= C::T - 4) | (c < 4) | (c >= C::T - 4);
+  unsigned char* ld = dst + ((r + 4) * C::S0 + c + 4) * C::PIX;
+  unsigned char* gd = P.xbuf + (((size_t)t.b * P.Hl + min(gy, P.Hl - 1)) * P.Wl + min(gx, P.Wl - 1)) * 64;
+#pragma unroll
+  for (int T = 0; T < 4; ++T) {
+    const int c0 = 16 * T + 4 * g;
+    const f4 bs = *reinterpret_cast<const f4*>(cst + kCstCompress + c0);
+    const f4 sc = *reinterpret_cast<const f4*>(cst + kCstCompress + 64 + c0);
+    float v[4];
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) v[r4] = act_value<MODE>(acc[T], r4, bs[r4], sc[r4], P.inv_out[0]);
+    const unsigned w = pack_codes4<MODE>(v);
+    *reinterpret_cast<unsigned*>(ld + c0) = inside ? w : 0u;
+    // device-scope store (sc1): written through to the device's coherence point, past this XCD's L2
+    if (inside & border) __hip_atomic_store(reinterpret_cast<unsigned*>(gd + c0), w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -451,21 +496,22 @@ __device__ __forceinline__ u4 project_phase(const unsigned char* slice, const h8
 
 // Frame-input compress (quantized policies).  Per group: stage -> features -> next group's RGB
 // loads issued -> per compress K-chunk, the project MFMAs of its phases and the compress MFMAs.
-template <int MODE, typename Tin, int TT = BodyFusedCfg<MODE>::T>
+// CORE: the T x T core only (compress exchange), else the whole region R0.
+template <int MODE, typename Tin, int TT = BodyFusedCfg<MODE>::T, bool CORE = false>
 __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst,
                                                 const float* cst, const typename BodyFusedCfg<MODE>::Frag* fr,
                                                 const h8 (&pf)[2], const Analysis& an, RgbStage<Tin>& stN,
                                                 unsigned char* slice, int* counter, int wave, int lane) {
   typedef BodyFusedCfg<MODE, TT> C;
-  constexpr int S = C::S0, N = S * S, G = (N + 15) / 16, NK = C::NKc;
+  constexpr int S = CORE ? C::T : C::S0, N = S * S, G = (N + 15) / 16, NK = C::NKc, O = CORE ? 0 : 4;
   static_assert(MODE != 0, "frame input serves the quantized policies");
   const int g = lane >> 4;
   const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
   for (int pg = wave, next; pg < G; pg = next) {
     stage_store<Tin>(stN, reinterpret_cast<float*>(slice), lane);
-    features_to_slice(slice, group_geom(t.y0 - 4, t.x0 - 4, S, pg).m, an, lane);
+    features_to_slice(slice, group_geom(t.y0 - O, t.x0 - O, S, pg).m, an, lane);
     next = claim_group(counter, lane);
-    if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, S, next), P, lane);
+    if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0 - O, t.x0 - O, S, next), P, lane);
     const f4 bs0 = *reinterpret_cast<const f4*>(cst + kCstProject + 4 * g);
     const f4 bs1 = *reinterpret_cast<const f4*>(cst + kCstProject + 16 + 4 * g);
     typename C::Acc acc[4];
@@ -498,7 +544,88 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
 #pragma unroll
       for (int T = 0; T < 4; ++T) acc[T] = mma<MODE>(fr[(T * NK + k) * 64 + lane], bop, acc[T]);
     }
-    compress_store<MODE, TT>(P, t, dst, cst, acc, pg, lane);
+    if constexpr (CORE) compress_store_core<MODE, TT>(P, t, dst, cst, acc, pg, lane);
+    else compress_store<MODE, TT>(P, t, dst, cst, acc, pg, lane);
+  }
+}
+
+// Compress exchange.  Each tile has computed compress on its core and stored the codes within 4
+// pixels of the core's edge to the exchange tensor with device-scope stores (sc1: written through
+// to the device's coherence point).  exchange_publish waits until this wave's stores are complete,
+// and after the block barrier stores the tile's launch count to its counter (device scope);
+// exchange_collect waits for the up to eight neighbours' counters to reach the same count, then
+// reads the 4-pixel ring of region R0 with device-scope loads (zero outside the low grid).  The
+// stores are complete before the counter is written and the loads are issued after the counters
+// were seen, and device-scope accesses are coherent across the XCDs' L2 caches, so no cache-wide
+// writeback or invalidate is needed.  Counters only grow: a tile reads its count at the start of
+// the launch (the launches before) and publishes one more, so nothing is reset between launches or
+// graph replays.  Every block of the launch is resident at once (one block per CU, no more tiles
+// than CUs); the wait is bounded all the same: if it runs out, xerr is set and the tile goes on.
+constexpr int kExchangeSpins = 1 << 16;
+__device__ __forceinline__ void exchange_publish(const BodyFusedArgs& P, int tidx, const int* counters, int tid) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  lds_barrier();
+  if (tid == 0) __hip_atomic_store(P.xflags + tidx, counters[10], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <int MODE, int TT>
+__device__ __forceinline__ void exchange_collect(const BodyFusedArgs& P, BodyTileF t, int tidx, int tx, int ty,
+                                                 unsigned char* dst, const int* counters, int tid, int wave,
+                                                 int lane) {
+  typedef BodyFusedCfg<MODE, TT> C;
+  if (wave == 0) {
+    const int target = counters[10];
+    const int per_frame = tx * ty, rem = tidx % per_frame, tyi = rem / tx, txi = rem - tyi * tx;
+    const int ny = tyi + lane / 3 - 1, nx = txi + lane % 3 - 1;
+    bool late = false;
+    if (lane < 9 && lane != 4 && ny >= 0 && ny < ty && nx >= 0 && nx < tx) {
+      const int* f = P.xflags + (tidx - rem) + ny * tx + nx;
+      for (int spin = 0; __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spin) {
+        if (spin >= kExchangeSpins) {
+          late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    if (late) __hip_atomic_fetch_or(P.xerr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  lds_barrier();
+  // ring pixels: 4 rows above and 4 below the core (S0 wide), 4 columns left and right of it;
+  // 16-byte chunks, 4 per pixel.  Pixels outside the low grid get an offset past the frame's
+  // range, which a raw buffer load returns as zero.
+  constexpr int S = C::S0, T = C::T, NR = 8 * S + 8 * T, Chunks = 4 * NR;
+  constexpr int PerT = (Chunks + C::Threads - 1) / C::Threads;
+  const int frame_bytes = P.Hl * P.Wl * 64;
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(P.xbuf + (size_t)t.b * frame_bytes, 0, frame_bytes, kRawBufferWord3);
+  u4 v[PerT];
+  int at[PerT];
+#pragma unroll
+  for (int j = 0; j < PerT; ++j) {
+    const int idx = min(tid + j * C::Threads, Chunks - 1), i = idx >> 2, k = idx & 3;
+    int r, c;
+    if (i < 8 * S) {                                   // rows 0..3 and T+4..T+7
+      const int row = i / S;
+      r = row < 4 ? row : T + row;
+      c = i - row * S;
+    } else {                                           // columns 0..3 and T+4..T+7 of rows 4..T+3
+      const int e = i - 8 * S, row = e >> 3, col = e & 7;
+      r = 4 + row;
+      c = col < 4 ? col : T + col;
+    }
+    const int gy = t.y0 - 4 + r, gx = t.x0 - 4 + c;
+    const bool inside = ((unsigned)gy < (unsigned)P.Hl) & ((unsigned)gx < (unsigned)P.Wl);
+    const int off = inside ? (gy * P.Wl + gx) * 64 + 16 * k : frame_bytes;
+    v[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kLoadDeviceScope));
+    at[j] = (r * S + c) * C::PIX + 16 * k;
+  }
+#pragma unroll
+  for (int j = 0; j < PerT; ++j) {
+    if (tid + j * C::Threads < Chunks) {
+      u2* d = reinterpret_cast<u2*>(dst + at[j]);      // 8-byte aligned (72-byte pixels)
+      d[0] = u2{v[j][0], v[j][1]};
+      d[1] = u2{v[j][2], v[j][3]};
+    }
   }
 }
 
@@ -687,12 +814,13 @@ __device__ __forceinline__ int body_tile_of(int b, int tiles, int first) {
 }
 
 // One output tile (tile index tidx of the launch part described by P).
-template <int MODE, int SRC, int TT>
+template <int MODE, int SRC, int TT, bool XC = false>
 __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   typedef BodyFusedCfg<MODE, TT> C;
   typedef typename std::conditional<SRC == (int)BodySrc::Frames32, float, _Float16>::type Tin;
   constexpr bool RGB = SRC != (int)BodySrc::Skip;
   static_assert(!RGB || MODE != 0, "frame input serves the quantized policies (FP16 project operands)");
+  static_assert(!XC || RGB, "the compress exchange serves the frame-input body");
   constexpr int CPT = (kBodyConsts + C::Threads - 1) / C::Threads;   // constants per thread
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* cst = reinterpret_cast<float*>(smem);
@@ -738,7 +866,8 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) pf[i] = reinterpret_cast<const h8*>(P.pfrag)[i * 64 + lane];
     an = analysis_from(P.analysis);
-    stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, C::S0, wave), P, lane);
+    if constexpr (XC) stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, C::T, wave), P, lane);
+    else stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, C::S0, wave), P, lane);
   } else {
     compress_fetch<MODE, TT>(rawN, P.skip + (size_t)t.b * (2 * P.Hl) * (2 * P.Wl) * 32, t, wave, P.Hl, P.Wl, lane);
   }
@@ -753,9 +882,17 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
       if (tid + j * C::Threads < FragChunks) fr_lds[tid + j * C::Threads] = fchunk[j];
   }
   if (tid < 10) counters[tid] = tid < 2 ? C::Waves : C::Waves / 2;
+  if (XC && tid == 0)                                  // this launch's count: the launches before + 1
+    counters[10] = __hip_atomic_load(P.xflags + tidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
   lds_barrier();
-  if constexpr (RGB) fb_compress_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
-  else fb_compress<MODE, TT>(P, t, bufA, cst, Fc, rawN, wave, lane);
+  if constexpr (XC) {
+    fb_compress_rgb<MODE, Tin, TT, true>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
+    exchange_publish(P, tidx, counters, tid);
+  } else if constexpr (RGB) {
+    fb_compress_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
+  } else {
+    fb_compress<MODE, TT>(P, t, bufA, cst, Fc, rawN, wave, lane);
+  }
   if constexpr (RGB) {                                 // expand weights: in flight during the barrier
     const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[5], C::FragBytes);
     const int voff = fresh(tid) * 16;
@@ -764,6 +901,7 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   }
   const int gf = (wave & 1) * 2 * C::NKg;              // this wave's group's first fragment
   const FragSet<MODE, 2 * C::NKg> F1 = load_frags<MODE, 2 * C::NKg>(P.frag[1], gf, lane);
+  if constexpr (XC) exchange_collect<MODE, TT>(P, t, tidx, tx, ty, bufA, counters, tid, wave, lane);
   lds_barrier();
   if constexpr (RGB) {                                 // compress no longer reads the region
 #pragma unroll
@@ -799,6 +937,12 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
 template <int MODE, int SRC, int TT = BodyFusedCfg<MODE>::T>
 __global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_kernel(BodyFusedArgs P) {
   body_tile<MODE, SRC, TT>(P, body_tile_of((int)blockIdx.x, (int)gridDim.x, 0));
+}
+
+// Frame-input body with the compress exchange (every block resident at once).
+template <int MODE, int SRC, int TT>
+__global__ __launch_bounds__(BodyFusedCfg<MODE>::Threads) void body_fused_xc_kernel(BodyFusedArgs P) {
+  body_tile<MODE, SRC, TT, true>(P, body_tile_of((int)blockIdx.x, (int)gridDim.x, 0));
 }
 
 // Two tile sides in one launch: blocks [0, n1) run tiles of side T1 for P1, the rest tiles of side
@@ -888,6 +1032,8 @@ int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus) {
 
 template <int MODE, int SRC, int TT>
 static const void* body_kernel_ptr() { return reinterpret_cast<const void*>(&body_fused_kernel<MODE, SRC, TT>); }
+template <int MODE, int SRC, int TT>
+static const void* body_xc_ptr() { return reinterpret_cast<const void*>(&body_fused_xc_kernel<MODE, SRC, TT>); }
 template <int MODE, int SRC, int T1, int T2>
 static const void* body_pair_ptr() { return reinterpret_cast<const void*>(&body_fused_pair_kernel<MODE, SRC, T1, T2>); }
 // dynamic LDS of a launch of tile side TT
@@ -914,7 +1060,13 @@ hipError_t body_fused_prepare() {
       {body_pair_ptr<0, 0, 16, 8>(), body_pair_lds<0, 0, 16, 8>()},
       {body_pair_ptr<1, 1, 24, 16>(), body_pair_lds<1, 1, 24, 16>()}, {body_pair_ptr<1, 2, 24, 16>(), body_pair_lds<1, 2, 24, 16>()},
       {body_pair_ptr<2, 1, 24, 16>(), body_pair_lds<2, 1, 24, 16>()}, {body_pair_ptr<2, 2, 24, 16>(), body_pair_lds<2, 2, 24, 16>()},
-      {body_pair_ptr<3, 1, 24, 16>(), body_pair_lds<3, 1, 24, 16>()}, {body_pair_ptr<3, 2, 24, 16>(), body_pair_lds<3, 2, 24, 16>()}};
+      {body_pair_ptr<3, 1, 24, 16>(), body_pair_lds<3, 1, 24, 16>()}, {body_pair_ptr<3, 2, 24, 16>(), body_pair_lds<3, 2, 24, 16>()},
+      {body_xc_ptr<1, 1, 24>(), BodyFusedCfg<1, 24>::LdsRgb}, {body_xc_ptr<1, 2, 24>(), BodyFusedCfg<1, 24>::LdsRgb},
+      {body_xc_ptr<2, 1, 24>(), BodyFusedCfg<2, 24>::LdsRgb}, {body_xc_ptr<2, 2, 24>(), BodyFusedCfg<2, 24>::LdsRgb},
+      {body_xc_ptr<3, 1, 24>(), BodyFusedCfg<3, 24>::LdsRgb}, {body_xc_ptr<3, 2, 24>(), BodyFusedCfg<3, 24>::LdsRgb},
+      {body_xc_ptr<1, 1, 16>(), BodyFusedCfg<1, 16>::LdsRgb}, {body_xc_ptr<1, 2, 16>(), BodyFusedCfg<1, 16>::LdsRgb},
+      {body_xc_ptr<2, 1, 16>(), BodyFusedCfg<2, 16>::LdsRgb}, {body_xc_ptr<2, 2, 16>(), BodyFusedCfg<2, 16>::LdsRgb},
+      {body_xc_ptr<3, 1, 16>(), BodyFusedCfg<3, 16>::LdsRgb}, {body_xc_ptr<3, 2, 16>(), BodyFusedCfg<3, 16>::LdsRgb}};
   for (const K& e : k) {
     const hipError_t r = hipFuncSetAttribute(e.fn, hipFuncAttributeMaxDynamicSharedMemorySize, e.lds);
     if (r != hipSuccess) return r;
@@ -964,6 +1116,39 @@ hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, i
     case 1: launch_body_m<1>(src, args, tile, tiles, stream); break;
     case 2: launch_body_m<2>(src, args, tile, tiles, stream); break;
     default: launch_body_m<3>(src, args, tile, tiles, stream); break;
+  }
+  return hipGetLastError();
+}
+
+template <int MODE, int SRC, int TT>
+static void launch_xc_t(const BodyFusedArgs& args, int tiles, hipStream_t stream) {
+  typedef BodyFusedCfg<MODE, TT> C;
+  constexpr int lds = C::LdsRgb;
+  hipLaunchKernelGGL((body_fused_xc_kernel<MODE, SRC, TT>), dim3(tiles), dim3(C::Threads), lds, stream, args);
+}
+template <int MODE>
+static void launch_xc_m(BodySrc src, const BodyFusedArgs& args, int tile, int tiles, hipStream_t stream) {
+  if (src == BodySrc::Frames16) {
+    if (tile == 16) launch_xc_t<MODE, 1, 16>(args, tiles, stream);
+    else launch_xc_t<MODE, 1, 24>(args, tiles, stream);
+  } else {
+    if (tile == 16) launch_xc_t<MODE, 2, 16>(args, tiles, stream);
+    else launch_xc_t<MODE, 2, 24>(args, tiles, stream);
+  }
+}
+
+hipError_t launch_body_fused_xc(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile, int cus,
+                                hipStream_t stream) {
+  // whole frames only, every tile resident at once (the LDS admits one block per CU)
+  if (mode == 0 || src == BodySrc::Skip || (tile != 24 && tile != 16)) return hipErrorInvalidValue;
+  if (args.row0 || args.rows || args.col0 || args.cols || !args.xbuf || !args.xflags || !args.xerr)
+    return hipErrorInvalidValue;
+  const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl, tile);
+  if (tiles > cus) return hipErrorInvalidValue;
+  switch (mode) {
+    case 1: launch_xc_m<1>(src, args, tile, tiles, stream); break;
+    case 2: launch_xc_m<2>(src, args, tile, tiles, stream); break;
+    default: launch_xc_m<3>(src, args, tile, tiles, stream); break;
   }
   return hipGetLastError();
 }

@@ -55,6 +55,11 @@ struct BodyFusedArgs {
   int H, W, py, px;        // frame geometry (frame-input variants)
   int row0, rows;          // low-grid rows this launch covers: [row0, row0 + rows); rows = 0: all
   int col0, cols;          // low-grid columns likewise: [col0, col0 + cols); cols = 0: all
+  // compress exchange (launch_body_fused_xc): each tile computes compress on its core only and takes
+  // the 4-pixel ring of its compress region from its neighbours' cores
+  unsigned char* xbuf;     // compress outputs of the tile cores' borders, [batch][Hl][Wl][64] bytes
+  int* xflags;             // per-tile launch counters (zeroed once; each launch adds one per tile)
+  unsigned* xerr;          // set when a neighbour wait ran out (results of that launch are invalid)
 };
 // tile = side of the body's output tile in low pixels (0: the policy's default, 24, or 16 for the FP16 policy)
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile = 0);
@@ -70,6 +75,11 @@ int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();
 hipError_t launch_body_fused(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile,
                              hipStream_t stream);
+// Frame-input body with the compress exchange (quantized policies, whole frames, tile 24 or 16): one
+// block per tile, every block resident at once (tiles <= CUs, one block per CU), neighbouring tiles
+// synchronised through args.xflags.
+hipError_t launch_body_fused_xc(int mode, BodySrc src, const BodyFusedArgs& args, int batch, int tile, int cus,
+                                hipStream_t stream);
 // two parts in one launch: batch1 frames (or a1's rows) on tile1 tiles, then batch2 frames (a2's
 // rows) on tile2 tiles; tiles (24, 16) for the quantized policies, (16, 8) for the FP16 policy
 hipError_t launch_body_fused_pair(int mode, BodySrc src, const BodyFusedArgs& a1, int batch1, int tile1,

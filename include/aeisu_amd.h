@@ -57,6 +57,10 @@ extern "C" {
                                             coefficients stay on chip.  KEEP_INTERMEDIATES implies it */
 #define AEISU_FLAG_BODY_TILE24 16u       /* frame-input body: always 24x24-low-pixel tiles (by default small
                                             frames take 16x16 tiles; parity tests run both) */
+#define AEISU_FLAG_BODY_NO_EXCHANGE 32u  /* frame-input body: every tile computes its whole compress halo (by
+                                            default, when a launch's tiles all fit on the device at once,
+                                            tiles take the halo ring from their neighbours; parity tests run
+                                            both) */
 
 /* intermediates for aeisu_copy_intermediate */
 #define AEISU_BUF_SKIP 0   /* FP16 [B][Hp/2][Wp/2][32] project output (not materialised on the

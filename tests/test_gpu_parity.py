@@ -118,14 +118,17 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
     (70x102 -> py = px = 29), frames narrower than one tile row and low grids that are not a multiple
     of the body tile (37x333, 200x72 in a batch of 3), with the body tiles these shapes select (16x16 for
     the small frames; 540p x 8 splits into 7 frames on 24x24 and 1 on 16x16 tiles, two launches) and with
-    24x24 tiles forced."""
+    24x24 tiles forced; each with the compress exchange between neighbouring tiles (the default where a
+    launch's tiles all fit on the device at once) and without it."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
     frames = torch.stack([_frame(h, w, 40 + i) for i in range(b)]).to(dt).cuda().contiguous()
     for model in (mixed_model, fp16_model, int8_model, fp8mma_model):
         unfused = model.run(frames, flags=L.FLAG_UNFUSED)
-        for flags, tile in ((0, "shape's tile"), (L.FLAG_BODY_TILE24, "24x24 tiles")):
+        for flags, tile in ((0, "shape's tile"), (L.FLAG_BODY_TILE24, "24x24 tiles"),
+                            (L.FLAG_BODY_NO_EXCHANGE, "shape's tile, no exchange"),
+                            (L.FLAG_BODY_TILE24 | L.FLAG_BODY_NO_EXCHANGE, "24x24 tiles, no exchange")):
             fused = model.run(frames, flags=flags)
             torch.cuda.synchronize()
             diff = (fused.float() - unfused.float()).abs().max().item()
@@ -215,12 +218,13 @@ def test_full_size_1080p_properties(mixed_model, int8_model, fp16_model, fp8mma_
     for model in (mixed_model, int8_model, fp16_model, fp8mma_model):
         fused = model.run(scene)
         unfused = model.run(scene, flags=L.FLAG_UNFUSED)
+        no_exchange = model.run(scene, flags=L.FLAG_BODY_NO_EXCHANGE)
         pair = model.run(both)
         flat_out = model.run(flat)
         torch.cuda.synchronize()
         say(f"  {model.precision}: max|fused - unfused| = {(fused.float() - unfused.float()).abs().max().item()}")
         assert fused.shape == (1, 3, 2160, 3840)
-        assert torch.equal(fused, unfused)
+        assert torch.equal(fused, unfused) and torch.equal(no_exchange, unfused)
         assert torch.isfinite(fused.float()).all() and fused.min().item() >= 0 and fused.max().item() <= 1
         assert torch.equal(pair[:1], fused) and torch.equal(pair[1:], flat_out)
     # flat field against the base of the artifact the Mixed runtime loaded
@@ -270,19 +274,23 @@ def test_fused_path_intermediates_and_stages(mixed_model, int8_model, fp8mma_mod
             assert model.intermediate(hd, L.BUF_SKIP).numel() > 0
 
 
-def test_batch_and_graph_consistency(fp16_model):
+def test_batch_and_graph_consistency(fp16_model, mixed_model):
+    """Batch independence, and graph replays against the eager result with eager frames in between
+    (the Mixed body's compress exchange counts launches, eager and replayed alike)."""
     say("case: batch-2 vs per-frame, graph vs eager")
     a, b = _frame(64, 64, 21), _frame(64, 64, 22)
     x = torch.stack((a, b)).half().cuda().contiguous()
-    both = fp16_model.run(x)
-    one = fp16_model.run(x[:1].contiguous())
-    two = fp16_model.run(x[1:].contiguous())
-    assert torch.equal(both[:1], one) and torch.equal(both[1:], two)
-    out = torch.empty_like(both)
-    for _ in range(3):
-        fp16_model.run(x, out=out, graph=True)
-        torch.cuda.synchronize()
-        assert torch.equal(out, both)
+    for model in (fp16_model, mixed_model):
+        both = model.run(x)
+        one = model.run(x[:1].contiguous())
+        two = model.run(x[1:].contiguous())
+        assert torch.equal(both[:1], one) and torch.equal(both[1:], two)
+        out = torch.empty_like(both)
+        for _ in range(3):
+            model.run(x, out=out, graph=True)
+            torch.cuda.synchronize()
+            assert torch.equal(out, both)
+            assert torch.equal(model.run(x), both)
 
 
 def test_nonfinite_input_raises(fp16_model):
