@@ -367,7 +367,7 @@ struct Scratch {
   void* work = nullptr;
   void* meta = nullptr;
   void* low[5] = {};
-  unsigned* nonfinite = nullptr;   // [0] non-finite output, [1] compress-exchange wait ran out
+  unsigned* nonfinite = nullptr;
   void* xbuf = nullptr;
   int* xflags = nullptr;
 };
@@ -715,7 +715,7 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
       (out_layout != AEISU_LAYOUT_NCHW_F16 && out_layout != AEISU_LAYOUT_NCHW_F32))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unsupported frame layout");
   if (flags & ~(AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_STAGE_TIMING | AEISU_FLAG_NO_PAD | AEISU_FLAG_UNFUSED |
-                AEISU_FLAG_BODY_TILE24 | AEISU_FLAG_BODY_NO_EXCHANGE))
+                AEISU_FLAG_BODY_TILE24 | AEISU_FLAG_BODY_NO_EXCHANGE | AEISU_FLAG_BODY_EXCHANGE_FALLBACK))
     fail(AEISU_ERR_INVALID_ARGUMENT, "unknown configure flag");
   const bool no_pad = flags & AEISU_FLAG_NO_PAD;
   if (no_pad && (height % 4 || width % 4))
@@ -774,6 +774,10 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
 
 static float inv(float s) { return 1.0f / s; }
 
+// Compress exchange: polls of a neighbour's counter before a tile computes its halo ring itself.  A
+// poll is one device-scope load (about a microsecond); neighbours normally publish within a few.
+constexpr int kExchangePolls = 128;
+
 // Low-buffer slot written by body layer li (0 compress, 1..4 bottlenecks).
 static int low_slot(const Geometry& g, int li) { return g.nlow == 5 ? li : (li % 2); }
 
@@ -810,7 +814,7 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     if (g.body_xc_tile) {                          // compress exchange between neighbouring tiles
       P.xbuf = static_cast<unsigned char*>(sc.xbuf);
       P.xflags = sc.xflags;
-      P.xerr = sc.nonfinite + 1;
+      P.xspins = (g.flags & AEISU_FLAG_BODY_EXCHANGE_FALLBACK) ? 0 : kExchangePolls;
       check_hip(launch_body_fused_xc(m, src, P, g.batch, g.body_xc_tile, g.cus, s), "fused body launch");
     } else if (g.body_cols24 > 0) {                       // right-hand columns on 16x16 tiles
       BodyFusedArgs Q = P;
@@ -950,8 +954,8 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.work.alloc(g.work_bytes());
   rt.meta.alloc(g.meta_bytes());
   for (int i = 0; i < 5; ++i) rt.low[i].alloc(i < g.nlow ? g.lowpx() * 64 * (mode == 0 ? 2 : 1) : 0);
-  rt.nonfinite.alloc(8);
-  check_hip(hipMemset(rt.nonfinite.ptr, 0, 8), "hipMemset(flags)");
+  rt.nonfinite.alloc(4);
+  check_hip(hipMemset(rt.nonfinite.ptr, 0, 4), "hipMemset(flag)");
   rt.xbuf.alloc(g.xbuf_bytes());
   rt.xflags.alloc(g.xflag_bytes());
   if (rt.xflags.ptr) check_hip(hipMemset(rt.xflags.ptr, 0, rt.xflags.bytes), "hipMemset(exchange counters)");
@@ -1147,20 +1151,17 @@ int aeisu_check_finite(aeisu_runtime* h, void* stream) {
   const int rc = guarded([&] {
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
-    unsigned flag[2] = {0u, 0u};
-    aeisu::check_hip(hipMemcpyAsync(flag, rt.nonfinite.ptr, 8, hipMemcpyDeviceToHost, (hipStream_t)stream), "flag readback");
+    unsigned flag = 0;
+    aeisu::check_hip(hipMemcpyAsync(&flag, rt.nonfinite.ptr, 4, hipMemcpyDeviceToHost, (hipStream_t)stream), "flag readback");
     aeisu::check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
-    if (flag[0] || flag[1]) {
-      aeisu::check_hip(hipMemsetAsync(rt.nonfinite.ptr, 0, 8, (hipStream_t)stream), "flag reset");
+    if (flag) {
+      aeisu::check_hip(hipMemsetAsync(rt.nonfinite.ptr, 0, 4, (hipStream_t)stream), "flag reset");
       aeisu::check_hip(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
-      status = flag[1] ? AEISU_ERR_HIP : AEISU_ERR_NONFINITE;
+      status = AEISU_ERR_NONFINITE;
     }
   });
   if (rc != AEISU_OK) return rc;
-  if (status == AEISU_ERR_HIP)
-    g_last_error = "fused body: a tile's wait for its neighbours' compress ran out (the frame is invalid)";
-  else if (status != AEISU_OK)
-    g_last_error = "Non-finite model reconstruction";
+  if (status != AEISU_OK) g_last_error = "Non-finite model reconstruction";
   return status;
 }
 

@@ -40,7 +40,7 @@
 // Compress exchange (body_fused_xc_kernel, frame input): when a whole-frame launch has no more tiles
 // than the device has CUs, every tile is resident at once, so a tile computes compress on its T x T
 // core only and takes the 4-pixel ring of R0 from its neighbours' cores through a device-memory
-// tensor (exchange_publish / exchange_collect): the compress work per tile drops from (T+8)^2 to
+// tensor (exchange_publish / exchange_wait / exchange_ring): the compress work per tile drops from (T+8)^2 to
 // T^2 pixels (1080p: 64 to 36 pixel groups).  The codes are the same, so the result is too.
 // 12 waves (3 per SIMD, up to 168 VGPRs each): compress and expand split the pixel groups over
 // all waves; in a grouped layer, wave w serves group w & 1 and keeps that group's 18 weight
@@ -553,25 +553,24 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
 // pixels of the core's edge to the exchange tensor with device-scope stores (sc1: written through
 // to the device's coherence point).  exchange_publish waits until this wave's stores are complete,
 // and after the block barrier stores the tile's launch count to its counter (device scope);
-// exchange_collect waits for the up to eight neighbours' counters to reach the same count, then
-// reads the 4-pixel ring of region R0 with device-scope loads (zero outside the low grid).  The
-// stores are complete before the counter is written and the loads are issued after the counters
-// were seen, and device-scope accesses are coherent across the XCDs' L2 caches, so no cache-wide
-// writeback or invalidate is needed.  Counters only grow: a tile reads its count at the start of
-// the launch (the launches before) and publishes one more, so nothing is reset between launches or
-// graph replays.  Every block of the launch is resident at once (one block per CU, no more tiles
-// than CUs); the wait is bounded all the same: if it runs out, xerr is set and the tile goes on.
-constexpr int kExchangeSpins = 1 << 16;
+// exchange_wait polls the up to eight neighbours' counters until they reach the same count, and
+// exchange_ring then reads the 4-pixel ring of region R0 with device-scope loads (zero outside the
+// low grid).  The stores are complete before the counter is written and the loads are issued after
+// the counters were seen, and device-scope accesses are coherent across the XCDs' L2 caches, so no
+// cache-wide writeback or invalidate is needed.  Counters only grow: a tile reads its count at the
+// start of the launch (the launches before) and publishes one more, so nothing is reset between
+// launches or graph replays.  Every block of the launch is resident at once (one block per CU, no
+// more tiles than CUs), and the wait is bounded all the same: after P.xspins polls (none if
+// P.xspins <= 0) the tile computes the ring itself, as without the exchange, so the result never
+// depends on the neighbours arriving in time.
 __device__ __forceinline__ void exchange_publish(const BodyFusedArgs& P, int tidx, const int* counters, int tid) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lds_barrier();
   if (tid == 0) __hip_atomic_store(P.xflags + tidx, counters[10], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-template <int MODE, int TT>
-__device__ __forceinline__ void exchange_collect(const BodyFusedArgs& P, BodyTileF t, int tidx, int tx, int ty,
-                                                 unsigned char* dst, const int* counters, int tid, int wave,
-                                                 int lane) {
-  typedef BodyFusedCfg<MODE, TT> C;
+// Block-uniform: true when every neighbour published this launch's count within the poll budget.
+__device__ __forceinline__ bool exchange_wait(const BodyFusedArgs& P, int tidx, int tx, int ty, int* counters,
+                                              int tid, int wave, int lane) {
   if (wave == 0) {
     const int target = counters[10];
     const int per_frame = tx * ty, rem = tidx % per_frame, tyi = rem / tx, txi = rem - tyi * tx;
@@ -579,17 +578,21 @@ __device__ __forceinline__ void exchange_collect(const BodyFusedArgs& P, BodyTil
     bool late = false;
     if (lane < 9 && lane != 4 && ny >= 0 && ny < ty && nx >= 0 && nx < tx) {
       const int* f = P.xflags + (tidx - rem) + ny * tx + nx;
-      for (int spin = 0; __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spin) {
-        if (spin >= kExchangeSpins) {
-          late = true;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
+      late = P.xspins <= 0;
+      for (int spin = 0; !late && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spin) {
+        if (spin >= P.xspins) late = true;
+        else __builtin_amdgcn_s_sleep(2);
       }
     }
-    if (late) __hip_atomic_fetch_or(P.xerr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool ready = __ballot(late) == 0ull;
+    if (tid == 0) counters[11] = ready;
   }
   lds_barrier();
+  return counters[11] != 0;
+}
+template <int MODE, int TT>
+__device__ __forceinline__ void exchange_ring(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst, int tid) {
+  typedef BodyFusedCfg<MODE, TT> C;
   // ring pixels: 4 rows above and 4 below the core (S0 wide), 4 columns left and right of it;
   // 16-byte chunks, 4 per pixel.  Pixels outside the low grid get an offset past the frame's
   // range, which a raw buffer load returns as zero.
@@ -900,8 +903,23 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
     for (int j = 0; j < FCPT; ++j) fchunk[j] = buffer_frag<u4>(r, voff, j * C::Threads * 16);
   }
   const int gf = (wave & 1) * 2 * C::NKg;              // this wave's group's first fragment
-  const FragSet<MODE, 2 * C::NKg> F1 = load_frags<MODE, 2 * C::NKg>(P.frag[1], gf, lane);
-  if constexpr (XC) exchange_collect<MODE, TT>(P, t, tidx, tx, ty, bufA, counters, tid, wave, lane);
+  FragSet<MODE, 2 * C::NKg> F1 = load_frags<MODE, 2 * C::NKg>(P.frag[1], gf, lane);
+  if constexpr (XC) {                                  // the weight loads above are in flight during the wait
+    if (exchange_wait(P, tidx, tx, ty, counters, tid, wave, lane)) {
+      exchange_ring<MODE, TT>(P, t, bufA, tid);
+    } else {                                           // block-uniform: compress the whole region here
+      if (tid == 0) counters[0] = C::Waves;
+      stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, C::S0, wave), P, fresh(lane));
+      lds_barrier();
+      fb_compress_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
+      // the weights are loaded again rather than kept live through that compress
+      const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[5], C::FragBytes);
+      const int voff = fresh(tid) * 16;
+#pragma unroll
+      for (int j = 0; j < FCPT; ++j) fchunk[j] = buffer_frag<u4>(r, voff, j * C::Threads * 16);
+      F1 = load_frags<MODE, 2 * C::NKg>(P.frag[1], gf, fresh(lane));
+    }
+  }
   lds_barrier();
   if constexpr (RGB) {                                 // compress no longer reads the region
 #pragma unroll
@@ -1141,7 +1159,7 @@ hipError_t launch_body_fused_xc(int mode, BodySrc src, const BodyFusedArgs& args
                                 hipStream_t stream) {
   // whole frames only, every tile resident at once (the LDS admits one block per CU)
   if (mode == 0 || src == BodySrc::Skip || (tile != 24 && tile != 16)) return hipErrorInvalidValue;
-  if (args.row0 || args.rows || args.col0 || args.cols || !args.xbuf || !args.xflags || !args.xerr)
+  if (args.row0 || args.rows || args.col0 || args.cols || !args.xbuf || !args.xflags)
     return hipErrorInvalidValue;
   const int tiles = body_fused_num_tiles(mode, batch, args.Hl, args.Wl, tile);
   if (tiles > cus) return hipErrorInvalidValue;

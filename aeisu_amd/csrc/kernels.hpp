@@ -59,7 +59,8 @@ struct BodyFusedArgs {
   // the 4-pixel ring of its compress region from its neighbours' cores
   unsigned char* xbuf;     // compress outputs of the tile cores' borders, [batch][Hl][Wl][64] bytes
   int* xflags;             // per-tile launch counters (zeroed once; each launch adds one per tile)
-  unsigned* xerr;          // set when a neighbour wait ran out (results of that launch are invalid)
+  int xspins;              // polls of a neighbour's counter before the tile computes its ring itself
+                           // (<= 0: always itself)
 };
 // tile = side of the body's output tile in low pixels (0: the policy's default, 24, or 16 for the FP16 policy)
 int body_fused_num_tiles(int mode, int batch, int Hl, int Wl, int tile = 0);

@@ -61,6 +61,9 @@ extern "C" {
                                             default, when a launch's tiles all fit on the device at once,
                                             tiles take the halo ring from their neighbours; parity tests run
                                             both) */
+#define AEISU_FLAG_BODY_EXCHANGE_FALLBACK 64u /* testing: with the compress exchange, every tile computes its
+                                            halo ring itself, as a tile does when its neighbours' compress
+                                            does not arrive in time (same result) */
 
 /* intermediates for aeisu_copy_intermediate */
 #define AEISU_BUF_SKIP 0   /* FP16 [B][Hp/2][Wp/2][32] project output (not materialised on the

@@ -119,7 +119,8 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
     of the body tile (37x333, 200x72 in a batch of 3), with the body tiles these shapes select (16x16 for
     the small frames; 540p x 8 splits into 7 frames on 24x24 and 1 on 16x16 tiles, two launches) and with
     24x24 tiles forced; each with the compress exchange between neighbouring tiles (the default where a
-    launch's tiles all fit on the device at once) and without it."""
+    launch's tiles all fit on the device at once), without it, and with every tile taking the exchange's
+    fallback (computing its halo ring itself, as when its neighbours do not arrive in time)."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
@@ -128,6 +129,7 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
         unfused = model.run(frames, flags=L.FLAG_UNFUSED)
         for flags, tile in ((0, "shape's tile"), (L.FLAG_BODY_TILE24, "24x24 tiles"),
                             (L.FLAG_BODY_NO_EXCHANGE, "shape's tile, no exchange"),
+                            (L.FLAG_BODY_EXCHANGE_FALLBACK, "shape's tile, exchange fallback"),
                             (L.FLAG_BODY_TILE24 | L.FLAG_BODY_NO_EXCHANGE, "24x24 tiles, no exchange")):
             fused = model.run(frames, flags=flags)
             torch.cuda.synchronize()
@@ -219,12 +221,13 @@ def test_full_size_1080p_properties(mixed_model, int8_model, fp16_model, fp8mma_
         fused = model.run(scene)
         unfused = model.run(scene, flags=L.FLAG_UNFUSED)
         no_exchange = model.run(scene, flags=L.FLAG_BODY_NO_EXCHANGE)
+        fallback = model.run(scene, flags=L.FLAG_BODY_EXCHANGE_FALLBACK)
         pair = model.run(both)
         flat_out = model.run(flat)
         torch.cuda.synchronize()
         say(f"  {model.precision}: max|fused - unfused| = {(fused.float() - unfused.float()).abs().max().item()}")
         assert fused.shape == (1, 3, 2160, 3840)
-        assert torch.equal(fused, unfused) and torch.equal(no_exchange, unfused)
+        assert torch.equal(fused, unfused) and torch.equal(no_exchange, unfused) and torch.equal(fallback, unfused)
         assert torch.isfinite(fused.float()).all() and fused.min().item() >= 0 and fused.max().item() <= 1
         assert torch.equal(pair[:1], fused) and torch.equal(pair[1:], flat_out)
     # flat field against the base of the artifact the Mixed runtime loaded
