@@ -241,6 +241,32 @@ def test_full_size_1080p_properties(mixed_model, int8_model, fp16_model, fp8mma_
         assert err <= 2 ** -11
 
 
+def test_body_exchange_selection(mixed_model, int8_model):
+    """The compress exchange is configured where a whole-frame body launch fits on the device (1080p,
+    720p and 540p at batch 1), not for batches whose tiles outnumber the CUs, not with the opt-out
+    flag, and its buffers (64 bytes per low pixel, a counter per tile) are counted in the persistent
+    bytes."""
+    from aeisu_amd import _lib as L
+    say("case: compress-exchange selection")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for model in (mixed_model, int8_model):
+        for b, h, w, flags, expect in ((1, 1080, 1920, 0, 24), (1, 540, 960, 0, 16), (8, 540, 960, 0, 0),
+                                       (1, 1080, 1920, L.FLAG_BODY_NO_EXCHANGE, 0)):
+            hd = model.handle(b, h, w, torch.float16, torch.float16, flags)
+            report = hd.report()
+            tile = int(report.split("body_exchange_tile=")[1].split()[0])
+            say(f"  {model.precision} {b}x{h}x{w} flags={flags}: exchange tile {tile}")
+            if cus >= 256:
+                assert tile == expect
+            if tile == 0:
+                continue
+            off = model.handle(b, h, w, torch.float16, torch.float16, flags | L.FLAG_BODY_NO_EXCHANGE)
+            hl, wl = (h + 32 + (32 - h % 32) % 32) // 4, (w + 32 + (32 - w % 32) % 32) // 4
+            tiles = b * -(-hl // tile) * -(-wl // tile)
+            extra = int(L.lib().aeisu_persistent_bytes(hd.ptr)) - int(L.lib().aeisu_persistent_bytes(off.ptr))
+            assert extra == b * hl * wl * 64 + 4 * tiles        # the cores' compress codes, counters
+
+
 def _artifact_base(name: str) -> np.ndarray:
     """[25, 4] reconstruction base of a SPYR8F8 artifact (tap, phase)."""
     t = spyr8f8.read_file(WEIGHTS / name)["tensors"]
