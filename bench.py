@@ -305,6 +305,11 @@ def main():
         log("bench: CPU baseline")
         cpu = cpu_baseline(torch.cat(pool_cpu)[:2], args.cpu_budget)
 
+    # the body's launch shape as configured (tile sides, halo exchange) from the startup report
+    report = dict(kv.split("=", 1) for kv in hd.report().split() if "=" in kv)
+    body_launch = {k: int(report[k]) for k in ("body_tiles24_frames", "body_tiles24_cols", "body_exchange_tile")
+                   if k in report}
+
     fps = B * 1000.0 / ms_per_step
     line = {
         "metric": "frames/s (ms/frame) 1080p->4K batch-1 mixed FP8/FP16; % MFMA / HBM roofline",
@@ -318,7 +323,7 @@ def main():
                    "batch": B, "input": [3, H, W],
                    "output": [3, 2 * H, 2 * W], "precision": wl["precision"], "weights": wl["weights"],
                    "timed": "graph replay" if graph else "eager launches",
-                   "refine_tail_head": "two kernels" if args.unfused else "fused"},
+                   "refine_tail_head": "two kernels" if args.unfused else "fused", "body_launch": body_launch},
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,
