@@ -357,7 +357,7 @@ struct Geometry {
   // compress exchange: the cores' compress codes (64 bytes per low pixel) and one counter per tile
   size_t xbuf_bytes() const { return body_xc_tile ? lowpx() * 64 : 0; }
   size_t xflag_bytes() const {
-    return body_xc_tile ? size_t(body_fused_num_tiles(2, batch, Hl, Wl, body_xc_tile)) * sizeof(int) : 0;
+    return body_xc_tile ? size_t(body_fused_num_tiles(2, batch, Hl, Wl, body_xc_tile)) * sizeof(unsigned) : 0;
   }
 };
 
@@ -369,7 +369,7 @@ struct Scratch {
   void* low[5] = {};
   unsigned* nonfinite = nullptr;
   void* xbuf = nullptr;
-  int* xflags = nullptr;
+  unsigned* xflags = nullptr;
 };
 
 struct Runtime {
@@ -416,7 +416,7 @@ struct Runtime {
     for (int i = 0; i < 5; ++i) sc.low[i] = low[i].ptr;
     sc.nonfinite = nonfinite.as<unsigned>();
     sc.xbuf = xbuf.ptr;
-    sc.xflags = xflags.as<int>();
+    sc.xflags = xflags.as<unsigned>();
     return sc;
   }
   size_t scratch_bytes() const {

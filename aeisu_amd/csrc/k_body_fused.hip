@@ -566,20 +566,22 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
 __device__ __forceinline__ void exchange_publish(const BodyFusedArgs& P, int tidx, const int* counters, int tid) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   lds_barrier();
-  if (tid == 0) __hip_atomic_store(P.xflags + tidx, counters[10], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(P.xflags + tidx, (unsigned)counters[10], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Block-uniform: true when every neighbour published this launch's count within the poll budget.
 __device__ __forceinline__ bool exchange_wait(const BodyFusedArgs& P, int tidx, int tx, int ty, int* counters,
                                               int tid, int wave, int lane) {
   if (wave == 0) {
-    const int target = counters[10];
+    const unsigned target = (unsigned)counters[10];
     const int per_frame = tx * ty, rem = tidx % per_frame, tyi = rem / tx, txi = rem - tyi * tx;
     const int ny = tyi + lane / 3 - 1, nx = txi + lane % 3 - 1;
     bool late = false;
     if (lane < 9 && lane != 4 && ny >= 0 && ny < ty && nx >= 0 && nx < tx) {
-      const int* f = P.xflags + (tidx - rem) + ny * tx + nx;
+      const unsigned* f = P.xflags + (tidx - rem) + ny * tx + nx;
       late = P.xspins <= 0;
-      for (int spin = 0; !late && __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target; ++spin) {
+      // counts wrap after 2^32 launches: compare the difference, which is -1 (behind) or 0
+      for (int spin = 0; !late && (int)(__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0;
+           ++spin) {
         if (spin >= P.xspins) late = true;
         else __builtin_amdgcn_s_sleep(2);
       }
@@ -886,7 +888,7 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   }
   if (tid < 10) counters[tid] = tid < 2 ? C::Waves : C::Waves / 2;
   if (XC && tid == 0)                                  // this launch's count: the launches before + 1
-    counters[10] = __hip_atomic_load(P.xflags + tidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+    counters[10] = (int)(__hip_atomic_load(P.xflags + tidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u);
   lds_barrier();
   if constexpr (XC) {
     fb_compress_rgb<MODE, Tin, TT, true>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);

@@ -58,7 +58,7 @@ struct BodyFusedArgs {
   // compress exchange (launch_body_fused_xc): each tile computes compress on its core only and takes
   // the 4-pixel ring of its compress region from its neighbours' cores
   unsigned char* xbuf;     // compress outputs of the tile cores' borders, [batch][Hl][Wl][64] bytes
-  int* xflags;             // per-tile launch counters (zeroed once; each launch adds one per tile)
+  unsigned* xflags;        // per-tile launch counters (zeroed once; each launch adds one per tile)
   int xspins;              // polls of a neighbour's counter before the tile computes its ring itself
                            // (<= 0: always itself)
 };
