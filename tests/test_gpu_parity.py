@@ -111,7 +111,8 @@ def test_head_phase_packing_exact(fp16_model, area_state):
 # fused kernels (body activations and coefficients on chip) vs the per-layer path
 # ------------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("h,w,b,fp32", [(72, 104, 1, False), (70, 102, 2, True), (37, 333, 1, False),
-                                         (540, 960, 1, False), (200, 72, 3, False), (540, 960, 8, False)])
+                                         (540, 960, 1, False), (200, 72, 3, False), (540, 960, 8, False),
+                                         (1080, 1920, 2, False)])
 def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model, h, w, b, fp32):
     """Same arithmetic, same rounding points: the fused body kernel and the fused refine+tail+head kernel
     must reproduce the per-layer path bit for bit in every policy, including odd padding offsets
@@ -119,8 +120,9 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
     of the body tile (37x333, 200x72 in a batch of 3), with the body tiles these shapes select (16x16 for
     the small frames; 540p x 8 splits into 7 frames on 24x24 and 1 on 16x16 tiles, two launches) and with
     24x24 tiles forced; each with the compress exchange between neighbouring tiles (the default where a
-    launch's tiles all fit on the device at once), without it, and with every tile taking the exchange's
-    fallback (computing its halo ring itself, as when its neighbours do not arrive in time)."""
+    launch's tiles all fit on the device at once; 1080p x 2 has more tiles than CUs and runs without it),
+    without it, and with every tile taking the exchange's fallback (computing its halo ring itself, as
+    when its neighbours do not arrive in time)."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
@@ -243,15 +245,15 @@ def test_full_size_1080p_properties(mixed_model, int8_model, fp16_model, fp8mma_
 
 def test_body_exchange_selection(mixed_model, int8_model):
     """The compress exchange is configured where a whole-frame body launch fits on the device (1080p,
-    720p and 540p at batch 1), not for batches whose tiles outnumber the CUs, not with the opt-out
-    flag, and its buffers (64 bytes per low pixel, a counter per tile) are counted in the persistent
-    bytes."""
+    720p and 540p at batch 1), not where the tiles outnumber the CUs (1440p, 540p x 8), not with the
+    opt-out flag, and its buffers (64 bytes per low pixel, a counter per tile) are counted in the
+    persistent bytes."""
     from aeisu_amd import _lib as L
     say("case: compress-exchange selection")
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     for model in (mixed_model, int8_model):
         for b, h, w, flags, expect in ((1, 1080, 1920, 0, 24), (1, 540, 960, 0, 16), (8, 540, 960, 0, 0),
-                                       (1, 1080, 1920, L.FLAG_BODY_NO_EXCHANGE, 0)):
+                                       (1, 1440, 2560, 0, 0), (1, 1080, 1920, L.FLAG_BODY_NO_EXCHANGE, 0)):
             hd = model.handle(b, h, w, torch.float16, torch.float16, flags)
             report = hd.report()
             tile = int(report.split("body_exchange_tile=")[1].split()[0])
