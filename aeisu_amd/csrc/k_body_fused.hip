@@ -712,12 +712,18 @@ __device__ __forceinline__ void expand_mma(const unsigned char* src, int qc, Fra
 }
 
 // work = fp16(dequant(expand output) + skip) for low pixel (ly, lx); sk[T] = the lane's four skip
-// channels of output tile T.
+// channels of output tile T.  Tile T holds phase T & 3, channels 16 (T >> 2) + 4g .. + 3 in lane
+// group g; one v_permlane16_swap per register pairs tiles T and T + 4 between groups 2k and 2k + 1,
+// after which group g holds 8 consecutive channels 16 (g & 1) + 8 (g >> 1) .. + 7 of phase T, and
+// the four groups of a pixel store the phase's 64 bytes in one 16-byte store each (the 8-byte stores
+// of the unpaired tiles write the same 33 MB at 1080p about 1.4 times slower).  Lanes of a pixel are
+// all active or all inactive, so the swap never reads an inactive partner.
 template <int MODE>
 __device__ __forceinline__ void expand_store(const BodyFusedArgs& P, int b, int ly, int lx, const float* cst,
                                              const typename BodyFusedCfg<MODE>::Acc (&acc)[8], const u2 (&sk)[8], int g) {
   const int Hq = 2 * P.Hl, Wq = 2 * P.Wl;
   const float inv_out = P.inv_out[5], s_out = P.s_out;
+  u2 wt[8];
 #pragma unroll
   for (int T = 0; T < 8; ++T) {
     const f4 bs = *reinterpret_cast<const f4*>(cst + kCstExpand + 16 * T + 4 * g);
@@ -743,10 +749,17 @@ __device__ __forceinline__ void expand_store(const BodyFusedArgs& P, int b, int 
         v[r4] = fmaf((float)qi, s_out, s[r4]);
       }
     }
-    u2 w;
-    w[0] = pack_h2(v[0], v[1]);
-    w[1] = pack_h2(v[2], v[3]);
-    *reinterpret_cast<u2*>(P.work + expand_offset(b, ly, lx, T, g, Hq, Wq)) = w;
+    wt[T][0] = pack_h2(v[0], v[1]);
+    wt[T][1] = pack_h2(v[2], v[3]);
+  }
+  const int c0 = 16 * (g & 1) + 8 * (g >> 1);
+#pragma unroll
+  for (int ph = 0; ph < 4; ++ph) {
+    unsigned x0 = wt[ph][0], x1 = wt[ph][1], y0 = wt[ph + 4][0], y1 = wt[ph + 4][1];
+    permlane16_swap_u(x0, y0);
+    permlane16_swap_u(x1, y1);
+    const size_t o = (((size_t)b * Hq + 2 * ly + (ph >> 1)) * Wq + 2 * lx + (ph & 1)) * 32 + c0;
+    *reinterpret_cast<u4*>(P.work + o) = u4{x0, x1, y0, y1};
   }
 }
 
