@@ -777,11 +777,25 @@ __device__ __forceinline__ void fb_expand(const BodyFusedArgs& P, BodyTileF t, c
     const int ly = t.y0 + r, lx = t.x0 + c;
     const bool store = q < N && ly < P.Hl && lx < P.Wl;
     const int lyc = min(ly, P.Hl - 1), lxc = min(lx, P.Wl - 1);
-    u2 sk[8];                                          // skip operands first: in flight during the MFMAs
+    // skip operands first (in flight during the MFMAs), as 16-byte loads of the channels
+    // 16 (g & 1) + 8 (g >> 1) .. + 7 of each phase, regrouped afterwards by the store's swap in
+    // reverse: lane group g then holds channels 4g..4g+3 (tile T) and 16+4g.. (tile T + 4)
+    u4 skr[4];
 #pragma unroll
-    for (int T = 0; T < 8; ++T) sk[T] = *reinterpret_cast<const u2*>(P.skip + expand_offset(t.b, lyc, lxc, T, g, Hq, Wq));
+    for (int ph = 0; ph < 4; ++ph)
+      skr[ph] = *reinterpret_cast<const u4*>(
+          P.skip + (((size_t)t.b * Hq + 2 * lyc + (ph >> 1)) * Wq + 2 * lxc + (ph & 1)) * 32 + 16 * (g & 1) + 8 * (g >> 1));
     typename C::Acc acc[8];
     expand_mma<MODE>(src, qc, [&](int i) { return F.f[i]; }, g, acc);
+    u2 sk[8];
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph) {
+      unsigned x0 = skr[ph][0], x1 = skr[ph][1], y0 = skr[ph][2], y1 = skr[ph][3];
+      permlane16_swap_u(x0, y0);
+      permlane16_swap_u(x1, y1);
+      sk[ph] = u2{x0, x1};
+      sk[ph + 4] = u2{y0, y1};
+    }
     if (store) expand_store<MODE>(P, t.b, ly, lx, cst, acc, sk, g);
   }
 }
