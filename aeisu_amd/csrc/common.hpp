@@ -192,6 +192,32 @@ __device__ __forceinline__ void coef_clamp_split(unsigned v, unsigned& u, unsign
   u = (ub & 0x7FFF7FFFu) | (v & 0x80008000u);
   w = (__builtin_bit_cast(unsigned, wm) & 0x7FFF7FFFu) | (v & 0x80008000u);
 }
+// Two FP16 coefficients (one dword) -> the clamped coefficients rounded to FP16, for the head of
+// the quantized policies (one FP16 B operand per coefficient instead of the exact u / w pair):
+//   c = v                                              for |v| <= 2
+//   c = sign(v) min(rne16((|v| - 2) h + 2), 2.5)       otherwise, h = fp16(0.05) = 0.0499877...,
+// one fused rounding (|v| - 2 is exact in FP16 for |v| >= 1); c(+-inf) = +-2.5, a NaN v gives a
+// quiet NaN.  The select is a minimum: rne16((m - 2) h + 2) >= m for m <= 2 and < m above, so
+// c = min(m, t, 2.5) on the magnitude m.  Differs from the FP32 clamp by at most half an FP16
+// ulp of c plus (0.05 - h)(|v| - 2) <= 1.2e-4, only where |v| > 2.
+__device__ __forceinline__ unsigned coef_clamp_h16(unsigned v) {
+  typedef unsigned short us2v __attribute__((ext_vector_type(2)));
+  const unsigned mb = v & 0x7FFF7FFFu;
+  const h2 m = __builtin_bit_cast(h2, mb);
+  const h2 two = {(_Float16)2.0f, (_Float16)2.0f};
+  const h2 h05 = {(_Float16)0.05f, (_Float16)0.05f};
+  // t >= 1.9 (or +inf) for every non-NaN m, so the minima run on the bit patterns (unsigned
+  // order = value order for non-negative FP16), which needs no NaN canonicalisation
+  const us2v t = __builtin_elementwise_min(__builtin_bit_cast(us2v, __builtin_elementwise_fma(m - two, h05, two)),
+                                           (us2v){0x4100, 0x4100});                    // min(., 2.5)
+  const us2v c = __builtin_elementwise_min(__builtin_bit_cast(us2v, mb), t);
+  const us2v nanpart = __builtin_elementwise_sub_sat(__builtin_bit_cast(us2v, mb), (us2v){0x7C00, 0x7C00});
+  unsigned cb;
+  asm("v_pk_mad_u16 %0, %1, %2, %3 clamp"
+      : "=v"(cb)
+      : "v"(__builtin_bit_cast(unsigned, nanpart)), "s"(0xFFFFFFFFu), "v"(__builtin_bit_cast(unsigned, c)));
+  return (cb & 0x7FFF7FFFu) | (v & 0x80008000u);
+}
 __device__ __forceinline__ float h2f_lo(unsigned w) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));
 }

@@ -335,6 +335,7 @@ struct Model {
 struct Geometry {
   int batch = 0, H = 0, W = 0, Hp = 0, Wp = 0, py = 0, px = 0, Hq = 0, Wq = 0, Hl = 0, Wl = 0;
   int in_fp32 = 0, out_fp32 = 0;
+  int qclamp = 0;                  // head of the quantized policies: clamped coefficients in FP16
   unsigned flags = 0;
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
                                    // (body activations and coefficients stay on chip)
@@ -639,7 +640,9 @@ static void pack_weights(ModeWeights& rt, const Artifact& a) {
   //                                               against the lane's own w and [1, 1] (group 0)
   // (clamp(a) = u + 0.05 w in the kernel).  Row m = 4g + i of tile t is (phase g, tap 4t + i);
   // taps 25..27 (tile 6, i > 0) are zero rows.  The accumulator lane (n, g) thus holds all 25
-  // taps of phase g for pixel n.
+  // taps of phase g for pixel n.  After the fragments (kHeadBankFrags of them): the FP32 base
+  // of those rows, float4 [g][t] = base[tap 4t + i][phase g], i = 0..3, the accumulator input
+  // of the quantized policies' head (A1 against [c ; c], c the clamped coefficient in FP16).
   {
     const float* K = basis.f32();  // [25][16][4]
     const float* B = base.f32();   // [25][4]
@@ -653,7 +656,7 @@ static void pack_weights(ModeWeights& rt, const Artifact& a) {
     auto lo = [](double v) {
       return f32_to_f16_bits((float)(v - (double)f16_bits_to_f32(f32_to_f16_bits((float)v))));
     };
-    rt.head.frag.upload(pack_frags<uint16_t>(14, 8, [&](int f, int m, int s) -> uint16_t {
+    std::vector<uint16_t> img = pack_frags<uint16_t>(kHeadBankFrags, 8, [&](int f, int m, int s) -> uint16_t {
       int tap, ph;
       row_of(f % 7, m, tap, ph);
       if (tap < 0) return 0;
@@ -666,7 +669,16 @@ static void pack_weights(ModeWeights& rt, const Artifact& a) {
       if (s == 4) return hi(B[tap * 4 + ph]);
       if (s == 5) return lo(B[tap * 4 + ph]);
       return 0;
-    }));
+    });
+    std::vector<float> basec(4 * 7 * 4, 0.f);
+    for (int g = 0; g < 4; ++g)
+      for (int t = 0; t < 7; ++t)
+        for (int i = 0; i < 4; ++i)
+          if (4 * t + i < 25) basec[(g * 7 + t) * 4 + i] = B[(4 * t + i) * 4 + g];
+    const size_t frag_halves = img.size();
+    img.resize(frag_halves + basec.size() * 2);
+    std::memcpy(img.data() + frag_halves, basec.data(), basec.size() * sizeof(float));
+    rt.head.frag.upload(img);
   }
 }
 
@@ -747,6 +759,7 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
   g.fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
   // the skip tensor only exists in device memory where the project kernel runs
   g.fused_rgb = g.fused && mode != 0;
+  g.qclamp = mode != 0;
   // low-resolution activations only reach device memory on the per-layer path
   g.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : (g.fused ? 0 : 2);
   const int low_groups = batch * g.Hl * ((g.Wl + 15) / 16);
@@ -755,7 +768,7 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
   g.grid.grouped = clamp_grid(grouped_num_tiles(batch, g.Hl, g.Wl), body_blocks_per_cu(1, mode), cus);
   g.grid.expand = clamp_grid((low_groups + 3) / 4, body_blocks_per_cu(2, mode), cus);
   g.grid.refine = clamp_grid(refine_num_tiles(batch, g.Hq, g.Wq), refine_blocks_per_cu(), cus);
-  g.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(g.in_fp32, g.out_fp32), cus);
+  g.grid.head = clamp_grid(head_num_tiles(batch, height, width), head_blocks_per_cu(g.in_fp32, g.out_fp32, g.qclamp), cus);
   const BodyPlan plan = (flags & AEISU_FLAG_BODY_TILE24) ? BodyPlan{batch, 0} : body_fused_plan(mode, batch, g.Hl, g.Wl, cus);
   g.body_split = plan.frames24;
   g.body_cols24 = plan.cols24;
@@ -899,7 +912,7 @@ static void enqueue_controller(const ModeWeights& w, const Geometry& g, const Sc
 
 static void enqueue_head(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in,
                          const void* d_meta, void* d_out, hipStream_t s) {
-  check_hip(launch_head(g.in_fp32, g.out_fp32, d_in, d_meta, w.head.frag.ptr, d_out, g.H, g.W, g.Hq, g.Wq,
+  check_hip(launch_head(g.in_fp32, g.out_fp32, g.qclamp, d_in, d_meta, w.head.frag.ptr, d_out, g.H, g.W, g.Hq, g.Wq,
                         g.py, g.px, g.batch, sc.nonfinite, g.grid.head, s), "head launch");
 }
 
@@ -913,7 +926,7 @@ static void enqueue_frame(const ModeWeights& w, const Geometry& g, const Scratch
   }
   // fused path: events 0, (1,) 3, 6 only; the head stage times refine + tail + head (3 -> 6)
   enqueue_body(w, g, sc, d_in, s, ev);
-  check_hip(launch_fused_tail_head(g.in_fp32, g.out_fp32, sc.work, d_in, w.refine_tail.frag.ptr,
+  check_hip(launch_fused_tail_head(g.in_fp32, g.out_fp32, g.qclamp, sc.work, d_in, w.refine_tail.frag.ptr,
                                    w.refine_tail.bias.as<float>(), w.tail_bias.as<float>(), w.head.frag.ptr, d_out,
                                    g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, g.grid.fused, s),
             "fused refine/tail/head launch");

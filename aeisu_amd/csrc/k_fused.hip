@@ -27,7 +27,14 @@
 //  * FP16 frames: QH = 6 (16 waves, 4 per SIMD, <= 128 VGPRs), the RGB tile stays FP16 in
 //    LDS and the head's FMAs take it as a mixed-precision operand (v_fma_mix, exact);
 //    FP32 frames: QH = 4 (12 waves) with an FP32 RGB tile.
+//  * Head synthesis, two forms (QC = false / true), each bit-identical to k_head.hip's:
+//    FP16 policy: the exact clamp split u + 0.05 w, two MFMAs per row tile (k_head.hip).
+//    Quantized policies (QC): the producers store the clamped coefficients rounded to FP16
+//    (common.hpp coef_clamp_h16), the consumer reads its 8 B-operand coefficients with one
+//    16-byte LDS read and runs ONE MFMA per row tile, [K_hi | K_lo] . [c ; c], with the FP32
+//    base (per lane group, 28 values) as the accumulator input.
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace aeisu {
 
@@ -130,7 +137,7 @@ __device__ __forceinline__ void patch_store(const PatchRegs<LY>& r, unsigned cha
 }
 
 // refine + tail for 16-pixel groups p*J .. p*J+J-1 of the tile (group q: packed row q/2, half q%2)
-template <typename LY>
+template <typename LY, bool QC>
 __device__ __forceinline__ void produce(const unsigned char* smem, const unsigned char* lds_patch,
                                         unsigned char* lds_meta, int p, int lane) {
   constexpr int J = LY::J;
@@ -181,6 +188,10 @@ __device__ __forceinline__ void produce(const unsigned char* smem, const unsigne
       u2 w;
       w[0] = pack_h2(o[0] + tb[0], o[1] + tb[1]);
       w[1] = pack_h2(o[2] + tb[2], o[3] + tb[3]);
+      if constexpr (QC) {                          // coefficients 4g..4g+3 of parity T, clamped
+        w[0] = coef_clamp_h16(w[0]);
+        w[1] = coef_clamp_h16(w[1]);
+      }
       *reinterpret_cast<u2*>(dst + 16 * T) = w;
     }
   }
@@ -248,10 +259,11 @@ __device__ __forceinline__ void fstore_pair<float>(__amdgpu_buffer_rsrc_t r, uns
 // Head on LR row `r` of the tile.  The four 16-pixel chunks are computed unconditionally
 // (every LDS address stays inside the tile buffers), so the row is one basic block the
 // scheduler can interleave; chunks or lanes past the frame edge only lose their stores.
-template <typename Tout, typename Rgb>
+// QC: A23 is unused and BC holds the lane group's FP32 base per row tile; otherwise BC is unused.
+template <typename Tout, typename Rgb, bool QC>
 __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const Rgb* lds_rgb, Tout* __restrict__ out,
                                             FusedTile t, const FusedGeom& G, int r, int lane, const h8 (&A1)[7],
-                                            const h8 (&A23)[7], const unsigned ones, float& chk) {
+                                            const h8 (&A23)[7], const f4 (&BC)[7], const unsigned ones, float& chk) {
   const int n = lane & 15, g = lane >> 4;
   const int y = 2 * t.qy0 + r - G.py;
   if (y < 0 || y >= G.H) return;                      // wave-uniform
@@ -262,24 +274,32 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
 #pragma unroll
   for (int j = 0; j < kFLW / 16; ++j) {
     const int x = 2 * t.qx0 + 16 * j - G.px + n;
-    const u2 coef = *reinterpret_cast<const u2*>(mrow + (8 * j + (n >> 1)) * kFMPix + 16 * (rho_y | (n & 1)) + 4 * g);
-    unsigned U[2], Wd[2];
-    coef_clamp_split(coef[0], U[0], Wd[0]);
-    coef_clamp_split(coef[1], U[1], Wd[1]);
-    unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
-#pragma unroll
-    for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
-#pragma unroll
-    for (int w = 0; w < 2; ++w) permlane16_swap_mfma(Ux[w], Uy[w]);
-    const u4 bu = {Ux[0], Ux[1], Uy[0], Uy[1]};
-    const u4 bw = {Wd[0], Wd[1], ones, 0u};
-    const h8 bop_u = __builtin_bit_cast(h8, bu);
-    const h8 bop_w = __builtin_bit_cast(h8, bw);
+    const _Float16* cpix = mrow + (8 * j + (n >> 1)) * kFMPix + 16 * (rho_y | (n & 1));
     f4 acc[7];
+    if constexpr (QC) {
+      // B slots 8g..8g+7 = clamped coefficients 8(g&1)..+7 (slots 16..31 repeat 0..15 for K_lo)
+      const h8 bop = *reinterpret_cast<const h8*>(cpix + 8 * (g & 1));
 #pragma unroll
-    for (int q = 0; q < 7; ++q) {
-      acc[q] = mfma_f16(A1[q], bop_u, f4{0.f, 0.f, 0.f, 0.f});
-      acc[q] = mfma_f16(A23[q], bop_w, acc[q]);
+      for (int q = 0; q < 7; ++q) acc[q] = mfma_f16(A1[q], bop, BC[q]);
+    } else {
+      const u2 coef = *reinterpret_cast<const u2*>(cpix + 4 * g);
+      unsigned U[2], Wd[2];
+      coef_clamp_split(coef[0], U[0], Wd[0]);
+      coef_clamp_split(coef[1], U[1], Wd[1]);
+      unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
+#pragma unroll
+      for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
+#pragma unroll
+      for (int w = 0; w < 2; ++w) permlane16_swap_mfma(Ux[w], Uy[w]);
+      const u4 bu = {Ux[0], Ux[1], Uy[0], Uy[1]};
+      const u4 bw = {Wd[0], Wd[1], ones, 0u};
+      const h8 bop_u = __builtin_bit_cast(h8, bu);
+      const h8 bop_w = __builtin_bit_cast(h8, bw);
+#pragma unroll
+      for (int q = 0; q < 7; ++q) {
+        acc[q] = mfma_f16(A1[q], bop_u, f4{0.f, 0.f, 0.f, 0.f});
+        acc[q] = mfma_f16(A23[q], bop_w, acc[q]);
+      }
     }
     const Rgb* L0 = lds_rgb + r * kFRW + 16 * j + n;
     // phase g of pixel n: the 25 taps in order (dy, dx) = (tap / 5, tap % 5)
@@ -316,7 +336,7 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
 }
 
 // Producer waves: coefficients of tile i+1, work patch of tile i+2.
-template <typename Tin>
+template <typename Tin, bool QC>
 __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float16* __restrict__ work,
                                               const FusedGeom& G, int wave, int lane, int ptid) {
   typedef FusedLayout<Tin> LY;
@@ -333,7 +353,7 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
     }
   }
   lds_barrier();                                   // weights, biases and prologue loads visible
-  if (t0 < G.num_tiles) produce<LY>(smem, smem + LY::OffPatch, smem + LY::OffMeta, wave, lane);
+  if (t0 < G.num_tiles) produce<LY, QC>(smem, smem + LY::OffPatch, smem + LY::OffMeta, wave, lane);
   lds_barrier();                                   // coefficients of tile 0 visible
   const int iters = tile_iters(G.num_tiles);
   for (int it = 0; it < iters; ++it) {
@@ -346,15 +366,15 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
     PatchRegs<LY> pr;
     if (tnn < G.num_tiles) patch_fetch<LY>(pr, work, fused_tile<LY::QH>(tnn, G), G, ptid_it);
     if (tn < G.num_tiles)
-      produce<LY>(smem, smem + LY::OffPatch + nxt * LY::SizePatch, smem + LY::OffMeta + nxt * LY::SizeMeta, wave,
-                  lane_it);
+      produce<LY, QC>(smem, smem + LY::OffPatch + nxt * LY::SizePatch, smem + LY::OffMeta + nxt * LY::SizeMeta,
+                      wave, lane_it);
     if (tnn < G.num_tiles) patch_store<LY>(pr, smem + LY::OffPatch + cur * LY::SizePatch, ptid_it);
     lds_barrier();
   }
 }
 
 // Consumer waves: head of tile i, RGB tile of tile i+1.
-template <typename Tin, typename Tout>
+template <typename Tin, typename Tout, bool QC>
 __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __restrict__ src,
                                               const h8* __restrict__ bankA, Tout* __restrict__ out,
                                               const FusedGeom& G, int row, int lane, int ctid,
@@ -363,10 +383,13 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
   typedef typename FusedCfg<Tin>::Rgb Rgb;
   const int g = lane >> 4;
   h8 A1[7], A23[7];
+  f4 BC[7];
+  const f4* basec = reinterpret_cast<const f4*>(bankA + kHeadBankFrags * 64);
 #pragma unroll
   for (int q = 0; q < 7; ++q) {
     A1[q] = bankA[q * 64 + lane];
-    A23[q] = bankA[(7 + q) * 64 + lane];
+    if constexpr (QC) BC[q] = basec[g * 7 + q];
+    else A23[q] = bankA[(7 + q) * 64 + lane];
   }
   const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
   float chk = 0.f;
@@ -386,9 +409,9 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
     const int cur = it & 1, nxt = cur ^ 1;
     RgbRegs<Tin, LY> rr;
     if (tn < G.num_tiles) rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(tn, G), G, ctid);
-    consume_row<Tout, Rgb>(smem + LY::OffMeta + cur * LY::SizeMeta,
-                           reinterpret_cast<const Rgb*>(smem + LY::OffRgb + cur * LY::SizeRgb), out,
-                           fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, ones, chk);
+    consume_row<Tout, Rgb, QC>(smem + LY::OffMeta + cur * LY::SizeMeta,
+                               reinterpret_cast<const Rgb*>(smem + LY::OffRgb + cur * LY::SizeRgb), out,
+                               fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, BC, ones, chk);
     if (tn < G.num_tiles) rgb_store<Tin, Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
     lds_barrier();
   }
@@ -396,7 +419,7 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
 }
 
 // Every wave executes the same number of barriers: two in the prologue, one per tile.
-template <typename Tin, typename Tout>
+template <typename Tin, typename Tout, bool QC>
 __global__ __launch_bounds__(FusedLayout<Tin>::Threads) void fused_tail_head_kernel(
     const _Float16* __restrict__ work, const Tin* __restrict__ src, const h8* __restrict__ rt_frag,
     const float* __restrict__ rbias, const float* __restrict__ tbias, const h8* __restrict__ bankA,
@@ -413,9 +436,10 @@ __global__ __launch_bounds__(FusedLayout<Tin>::Threads) void fused_tail_head_ker
     else if (tid < 128) b[tid] = tbias[tid - 64];
   }
   if (wave < kFProducers)                            // wave-uniform role
-    producer_main<Tin>(smem, work, G, wave, lane, tid);
+    producer_main<Tin, QC>(smem, work, G, wave, lane, tid);
   else
-    consumer_main<Tin, Tout>(smem, src, bankA, out, G, wave - kFProducers, lane, tid - 64 * kFProducers, nonfinite);
+    consumer_main<Tin, Tout, QC>(smem, src, bankA, out, G, wave - kFProducers, lane, tid - 64 * kFProducers,
+                                 nonfinite);
 }
 
 static FusedGeom fused_geometry(int qh, int H, int W, int Hq, int Wq, int py, int px, int batch) {
@@ -435,13 +459,13 @@ int fused_num_tiles(int in_fp32, int batch, int H, int W, int Hq, int Wq, int py
   return fused_geometry(qh, H, W, Hq, Wq, py, px, batch).num_tiles;
 }
 
-template <typename Tin, typename Tout>
+template <typename Tin, typename Tout, bool QC>
 static hipError_t launch_fused_t(const void* work, const void* src, const void* rt_frag, const float* rbias,
                                  const float* tbias, const void* bankA, void* out, int H, int W, int Hq, int Wq,
                                  int py, int px, int batch, unsigned* nonfinite, int grid, hipStream_t stream) {
   typedef FusedLayout<Tin> LY;
   const FusedGeom G = fused_geometry(LY::QH, H, W, Hq, Wq, py, px, batch);
-  hipLaunchKernelGGL((fused_tail_head_kernel<Tin, Tout>), dim3(grid), dim3(LY::Threads), LY::Lds, stream,
+  hipLaunchKernelGGL((fused_tail_head_kernel<Tin, Tout, QC>), dim3(grid), dim3(LY::Threads), LY::Lds, stream,
                      (const _Float16*)work, (const Tin*)src, (const h8*)rt_frag, rbias, tbias, (const h8*)bankA,
                      (Tout*)out, G, nonfinite);
   return hipGetLastError();
@@ -449,29 +473,41 @@ static hipError_t launch_fused_t(const void* work, const void* src, const void* 
 
 // Allows the kernels' dynamic LDS above the default limit; called once per device at configure.
 hipError_t fused_prepare() {
-  const void* k[4] = {reinterpret_cast<const void*>(&fused_tail_head_kernel<float, float>),
-                      reinterpret_cast<const void*>(&fused_tail_head_kernel<float, _Float16>),
-                      reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, float>),
-                      reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, _Float16>)};
-  const int lds[4] = {FusedLayout<float>::Lds, FusedLayout<float>::Lds, FusedLayout<_Float16>::Lds,
-                      FusedLayout<_Float16>::Lds};
-  for (int i = 0; i < 4; ++i) {
+  const void* k[8] = {reinterpret_cast<const void*>(&fused_tail_head_kernel<float, float, false>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<float, _Float16, false>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, float, false>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, _Float16, false>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<float, float, true>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<float, _Float16, true>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, float, true>),
+                      reinterpret_cast<const void*>(&fused_tail_head_kernel<_Float16, _Float16, true>)};
+  const int lds[8] = {FusedLayout<float>::Lds,    FusedLayout<float>::Lds,    FusedLayout<_Float16>::Lds,
+                      FusedLayout<_Float16>::Lds, FusedLayout<float>::Lds,    FusedLayout<float>::Lds,
+                      FusedLayout<_Float16>::Lds, FusedLayout<_Float16>::Lds};
+  for (int i = 0; i < 8; ++i) {
     const hipError_t e = hipFuncSetAttribute(k[i], hipFuncAttributeMaxDynamicSharedMemorySize, lds[i]);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
 
-hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, const void* work, const void* src, const void* rt_frag,
-                                  const float* rbias, const float* tbias, const void* bankA, void* out, int H, int W,
-                                  int Hq, int Wq, int py, int px, int batch, unsigned* nonfinite, int grid,
-                                  hipStream_t stream) {
-#define AEISU_FUSED(TI, TO) \
-  launch_fused_t<TI, TO>(work, src, rt_frag, rbias, tbias, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream)
-  if (in_fp32 && out_fp32) return AEISU_FUSED(float, float);
-  if (in_fp32) return AEISU_FUSED(float, _Float16);
-  if (out_fp32) return AEISU_FUSED(_Float16, float);
-  return AEISU_FUSED(_Float16, _Float16);
+hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, int qclamp, const void* work, const void* src,
+                                  const void* rt_frag, const float* rbias, const float* tbias, const void* bankA,
+                                  void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
+                                  unsigned* nonfinite, int grid, hipStream_t stream) {
+#define AEISU_FUSED(TI, TO, QC) \
+  launch_fused_t<TI, TO, QC>(work, src, rt_frag, rbias, tbias, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, \
+                             grid, stream)
+  if (qclamp) {
+    if (in_fp32 && out_fp32) return AEISU_FUSED(float, float, true);
+    if (in_fp32) return AEISU_FUSED(float, _Float16, true);
+    if (out_fp32) return AEISU_FUSED(_Float16, float, true);
+    return AEISU_FUSED(_Float16, _Float16, true);
+  }
+  if (in_fp32 && out_fp32) return AEISU_FUSED(float, float, false);
+  if (in_fp32) return AEISU_FUSED(float, _Float16, false);
+  if (out_fp32) return AEISU_FUSED(_Float16, float, false);
+  return AEISU_FUSED(_Float16, _Float16, false);
 #undef AEISU_FUSED
 }
 

@@ -32,12 +32,18 @@
 //    2-pixel clamped halo) and each lane's FP16 coefficients of the NEXT tile
 //    are loaded into registers while the current tile is computed, and the RGB
 //    tile is double-buffered in LDS (one barrier per tile).
+//  * Quantized policies (QC): the clamp is coef_clamp_h16 (the clamped coefficient rounded to
+//    FP16, <= 1.2e-4 + half an FP16 ulp from the FP32 clamp, only for |a| > 2).  Lane (n, g)
+//    reads and clamps coefficients 8(g&1)..+7 itself (no exchange), and each row tile takes ONE
+//    MFMA, [K_hi | K_lo] . [c ; c], with the FP32 base of its rows as the accumulator input
+//    (bank image: the 14 fragments, then base[g][t] as 4 x 7 float4).
 //  * Output: lane groups (0, 1) and (2, 3) hold horizontally adjacent output pixels
 //    (phases TL/TR, BL/BR); one permlane16 swap pairs them, so groups 0 and 2 each store
 //    two values per channel.  A per-lane
 //    running sum 0 * output (NaN for any non-finite output) sets the nonfinite
 //    flag once per wave at the end.
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace aeisu {
 
@@ -46,8 +52,6 @@ constexpr int kHeadLW = kHeadTW + 4, kHeadLH = kHeadTH + 4;
 constexpr int kHeadLPos = kHeadLW * kHeadLH;              // RGB positions per tile (with halo)
 constexpr int kHeadFill = (kHeadLPos + 255) / 256;        // positions loaded per thread
 constexpr int kHeadChunks = kHeadTW / 16;
-// bank image: 7 K=32 fragments (h8 per lane), then 7 + 7 K=16 fragments (h4 per lane)
-constexpr int kHeadFragBytes = 7 * 64 * 16 + 14 * 64 * 8;
 
 template <typename Tin>
 __device__ __forceinline__ float load_px(const Tin* p) { return (float)*p; }
@@ -66,13 +70,15 @@ __device__ __forceinline__ HeadTile head_tile(int tidx, int tiles_x, int tiles_y
 }
 
 // Registers holding one tile's inputs ahead of its computation.
+template <bool QC>
 struct HeadPrefetch {
   float rgb[kHeadFill][3];   // this thread's share of the clamped RGB tile
-  u2 coef[kHeadChunks];      // this lane's 4 FP16 coefficients for each chunk of its row
+  // this lane's FP16 coefficients for each chunk of its row: 4g..4g+3, or 8(g&1)..+7 (QC)
+  typename std::conditional<QC, u4, u2>::type coef[kHeadChunks];
 };
 
-template <typename Tin>
-__device__ __forceinline__ void head_fetch(HeadPrefetch& p, const Tin* __restrict__ src,
+template <bool QC, typename Tin>
+__device__ __forceinline__ void head_fetch(HeadPrefetch<QC>& p, const Tin* __restrict__ src,
                                            const _Float16* __restrict__ meta, HeadTile t, int H, int W,
                                            int Hq, int Wq, int py, int px, int wave, int n, int g) {
   const size_t plane = (size_t)H * W;
@@ -97,7 +103,9 @@ __device__ __forceinline__ void head_fetch(HeadPrefetch& p, const Tin* __restric
   for (int j = 0; j < kHeadChunks; ++j) {
     const int X = min(t.x0 + 16 * j + n, W - 1) + px;
     const int rho = ((Y & 1) << 1) | (X & 1);
-    p.coef[j] = *reinterpret_cast<const u2*>(mrow + (size_t)(X >> 1) * 64 + 16 * rho + 4 * g);
+    const _Float16* c = mrow + (size_t)(X >> 1) * 64 + 16 * rho;
+    if constexpr (QC) p.coef[j] = *reinterpret_cast<const u4*>(c + 8 * (g & 1));
+    else p.coef[j] = *reinterpret_cast<const u2*>(c + 4 * g);
   }
 }
 
@@ -112,7 +120,7 @@ __device__ __forceinline__ void store_pair<float>(float* p, float left, float ri
   *reinterpret_cast<float2*>(p) = make_float2(left, right);
 }
 
-template <typename Tin, typename Tout>
+template <typename Tin, typename Tout, bool QC>
 __global__ __launch_bounds__(256, 3) void head_kernel(
     const Tin* __restrict__ src, const _Float16* __restrict__ meta, const h8* __restrict__ bankA,
     Tout* __restrict__ out, int H, int W, int Hq, int Wq, int py, int px, int batch,
@@ -121,10 +129,13 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   h8 A1[7], A23[7];  // [K_hi | K_lo] and [(0.05K)_hi of 4g..4g+3, base_hi, base_lo, 0, 0] per lane group
+  f4 BC[7];          // QC: FP32 base of the lane group's rows per row tile (instead of A23)
+  const f4* basec = reinterpret_cast<const f4*>(bankA + kHeadBankFrags * 64);
 #pragma unroll
   for (int t = 0; t < 7; ++t) {
     A1[t] = bankA[t * 64 + lane];
-    A23[t] = bankA[(7 + t) * 64 + lane];
+    if constexpr (QC) BC[t] = basec[g * 7 + t];
+    else A23[t] = bankA[(7 + t) * 64 + lane];
   }
   const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
   float chk = 0.f;   // 0 * every output of this lane: NaN iff one was not finite
@@ -135,7 +146,7 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
   const size_t oplane = (size_t)4 * H * W;
 
   int tidx = tile_of(0, num_tiles);
-  HeadPrefetch cur;
+  HeadPrefetch<QC> cur;
   if (tidx < num_tiles)
     head_fetch(cur, src, meta, head_tile(tidx, tiles_x, tiles_y), H, W, Hq, Wq, py, px, wave, n, g);
 
@@ -148,7 +159,8 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
       const int q = threadIdx.x + 256 * k;
       if (q < kHeadLPos) buf[q] = make_float4(cur.rgb[k][0], cur.rgb[k][1], cur.rgb[k][2], 0.f);
     }
-    const u2 coef[kHeadChunks] = {cur.coef[0], cur.coef[1], cur.coef[2], cur.coef[3]};
+    const typename std::conditional<QC, u4, u2>::type coef[kHeadChunks] = {cur.coef[0], cur.coef[1], cur.coef[2],
+                                                                            cur.coef[3]};
     const int ntidx = tile_of(it + 1, num_tiles);
     if (ntidx < num_tiles)
       head_fetch(cur, src, meta, head_tile(ntidx, tiles_x, tiles_y), H, W, Hq, Wq, py, px, wave, n, g);
@@ -161,25 +173,34 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
       for (int j = 0; j < kHeadChunks; ++j) {
         if (t.x0 + 16 * j >= W) break;               // wave-uniform
         const int x = t.x0 + 16 * j + n;
-        // coefficients 4g..4g+3 of pixel n -> (u, w) halves
-        unsigned U[2], Wd[2];
-        coef_clamp_split(coef[j][0], U[0], Wd[0]);
-        coef_clamp_split(coef[j][1], U[1], Wd[1]);
-        // u of groups 0..3 -> group g holds u[8(g&1) .. 8(g&1)+7]
-        unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
-#pragma unroll
-        for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
-#pragma unroll
-        for (int w = 0; w < 2; ++w) permlane16_swap_mfma(Ux[w], Uy[w]);
-        const u4 bu = {Ux[0], Ux[1], Uy[0], Uy[1]};
-        const u4 bw = {Wd[0], Wd[1], ones, 0u};
-        const h8 bop_u = __builtin_bit_cast(h8, bu);
-        const h8 bop_w = __builtin_bit_cast(h8, bw);
         f4 acc[7];
+        if constexpr (QC) {
+          // coefficients 8(g&1)..+7 of pixel n, clamped: B slots 8g..8g+7 (K_lo repeats K_hi's)
+          const u4 cw = {coef_clamp_h16(coef[j][0]), coef_clamp_h16(coef[j][1]), coef_clamp_h16(coef[j][2]),
+                         coef_clamp_h16(coef[j][3])};
+          const h8 bop = __builtin_bit_cast(h8, cw);
 #pragma unroll
-        for (int r = 0; r < 7; ++r) {
-          acc[r] = mfma_f16(A1[r], bop_u, f4{0.f, 0.f, 0.f, 0.f});
-          acc[r] = mfma_f16(A23[r], bop_w, acc[r]);
+          for (int r = 0; r < 7; ++r) acc[r] = mfma_f16(A1[r], bop, BC[r]);
+        } else {
+          // coefficients 4g..4g+3 of pixel n -> (u, w) halves
+          unsigned U[2], Wd[2];
+          coef_clamp_split(coef[j][0], U[0], Wd[0]);
+          coef_clamp_split(coef[j][1], U[1], Wd[1]);
+          // u of groups 0..3 -> group g holds u[8(g&1) .. 8(g&1)+7]
+          unsigned Ux[2] = {U[0], U[1]}, Uy[2] = {U[0], U[1]};
+#pragma unroll
+          for (int w = 0; w < 2; ++w) permlane32_swap_mfma(Ux[w], Uy[w]);
+#pragma unroll
+          for (int w = 0; w < 2; ++w) permlane16_swap_mfma(Ux[w], Uy[w]);
+          const u4 bu = {Ux[0], Ux[1], Uy[0], Uy[1]};
+          const u4 bw = {Wd[0], Wd[1], ones, 0u};
+          const h8 bop_u = __builtin_bit_cast(h8, bu);
+          const h8 bop_w = __builtin_bit_cast(h8, bw);
+#pragma unroll
+          for (int r = 0; r < 7; ++r) {
+            acc[r] = mfma_f16(A1[r], bop_u, f4{0.f, 0.f, 0.f, 0.f});
+            acc[r] = mfma_f16(A23[r], bop_w, acc[r]);
+          }
         }
         const float4* L0 = buf + wave * kHeadLW + 16 * j + n;
         // phase g of pixel n: the 25 taps in order (dy, dx) = (tap / 5, tap % 5)
@@ -213,11 +234,11 @@ __global__ __launch_bounds__(256, 3) void head_kernel(
   if (nonfinite && __ballot(chk != chk) != 0ull && lane == 0) atomicOr(nonfinite, 1u);
 }
 
-template <typename Tin, typename Tout>
+template <typename Tin, typename Tout, bool QC>
 hipError_t launch_head_t(const void* src, const void* meta, const void* bankA, void* out, int H, int W,
                          int Hq, int Wq, int py, int px, int batch, unsigned* nonfinite, int grid,
                          hipStream_t stream) {
-  hipLaunchKernelGGL((head_kernel<Tin, Tout>), dim3(grid), dim3(256), 0, stream, (const Tin*)src,
+  hipLaunchKernelGGL((head_kernel<Tin, Tout, QC>), dim3(grid), dim3(256), 0, stream, (const Tin*)src,
                      (const _Float16*)meta, (const h8*)bankA, (Tout*)out, H, W, Hq, Wq, py, px, batch,
                      nonfinite);
   return hipGetLastError();
@@ -227,25 +248,35 @@ int head_num_tiles(int batch, int H, int W) {
   return batch * ((H + kHeadTH - 1) / kHeadTH) * ((W + kHeadTW - 1) / kHeadTW);
 }
 
-hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* meta, const void* bankA,
+hipError_t launch_head(int in_fp32, int out_fp32, int qclamp, const void* src, const void* meta, const void* bankA,
                        void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
                        unsigned* nonfinite, int grid, hipStream_t stream) {
-  if (in_fp32 && out_fp32)
-    return launch_head_t<float, float>(src, meta, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream);
-  if (in_fp32)
-    return launch_head_t<float, _Float16>(src, meta, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream);
-  if (out_fp32)
-    return launch_head_t<_Float16, float>(src, meta, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream);
-  return launch_head_t<_Float16, _Float16>(src, meta, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream);
+#define AEISU_HEAD(TI, TO, QC) \
+  launch_head_t<TI, TO, QC>(src, meta, bankA, out, H, W, Hq, Wq, py, px, batch, nonfinite, grid, stream)
+  if (qclamp) {
+    if (in_fp32 && out_fp32) return AEISU_HEAD(float, float, true);
+    if (in_fp32) return AEISU_HEAD(float, _Float16, true);
+    if (out_fp32) return AEISU_HEAD(_Float16, float, true);
+    return AEISU_HEAD(_Float16, _Float16, true);
+  }
+  if (in_fp32 && out_fp32) return AEISU_HEAD(float, float, false);
+  if (in_fp32) return AEISU_HEAD(float, _Float16, false);
+  if (out_fp32) return AEISU_HEAD(_Float16, float, false);
+  return AEISU_HEAD(_Float16, _Float16, false);
+#undef AEISU_HEAD
 }
 
-int head_blocks_per_cu(int in_fp32, int out_fp32) {
+template <bool QC>
+static hipError_t head_occupancy(int& n, int in_fp32, int out_fp32) {
+  if (in_fp32 && out_fp32) return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<float, float, QC>, 256, 0);
+  if (in_fp32) return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<float, _Float16, QC>, 256, 0);
+  if (out_fp32) return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<_Float16, float, QC>, 256, 0);
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<_Float16, _Float16, QC>, 256, 0);
+}
+
+int head_blocks_per_cu(int in_fp32, int out_fp32, int qclamp) {
   int n = 0;
-  hipError_t e;
-  if (in_fp32 && out_fp32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<float, float>, 256, 0);
-  else if (in_fp32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<float, _Float16>, 256, 0);
-  else if (out_fp32) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<_Float16, float>, 256, 0);
-  else e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, head_kernel<_Float16, _Float16>, 256, 0);
+  const hipError_t e = qclamp ? head_occupancy<true>(n, in_fp32, out_fp32) : head_occupancy<false>(n, in_fp32, out_fp32);
   return e == hipSuccess && n > 0 ? n : 1;
 }
 

@@ -22,7 +22,12 @@ hipError_t launch_expand(int mode, const void* low, const void* skip, const void
                          int grid, hipStream_t stream);
 hipError_t launch_refine_tail(const void* work, const void* wfrag, const float* rbias, const float* tbias,
                               void* meta, int Hq, int Wq, int batch, int grid, hipStream_t stream);
-hipError_t launch_head(int in_fp32, int out_fp32, const void* src, const void* meta, const void* bankA,
+// Head bank image (engine.cpp): kHeadBankFrags MFMA fragments of 64 lanes x 8 FP16, then the FP32 base of
+// each lane group's rows per row tile (float4 [4][7]) for the quantized policies' head (qclamp).
+constexpr int kHeadBankFrags = 14;
+// qclamp: quantized policies' head (clamped coefficients rounded to FP16, one MFMA per row tile);
+// 0: the FP16 policy's exact clamp split.
+hipError_t launch_head(int in_fp32, int out_fp32, int qclamp, const void* src, const void* meta, const void* bankA,
                        void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
                        unsigned* nonfinite, int grid, hipStream_t stream);
 
@@ -90,13 +95,13 @@ hipError_t launch_body_fused_pair(int mode, BodySrc src, const BodyFusedArgs& a1
 // frames, 768 for FP32 frames).
 int fused_num_tiles(int in_fp32, int batch, int H, int W, int Hq, int Wq, int py, int px);
 hipError_t fused_prepare();
-hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, const void* work, const void* src, const void* rt_frag,
-                                  const float* rbias, const float* tbias, const void* bankA, void* out, int H, int W,
-                                  int Hq, int Wq, int py, int px, int batch, unsigned* nonfinite, int grid,
-                                  hipStream_t stream);
+hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, int qclamp, const void* work, const void* src,
+                                  const void* rt_frag, const float* rbias, const float* tbias, const void* bankA,
+                                  void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
+                                  unsigned* nonfinite, int grid, hipStream_t stream);
 
 // Resident blocks per CU (occupancy), used to size the persistent grids.
-int head_blocks_per_cu(int in_fp32, int out_fp32);
+int head_blocks_per_cu(int in_fp32, int out_fp32, int qclamp);
 int project_blocks_per_cu(int in_fp32, int precise);
 int refine_blocks_per_cu();
 int body_blocks_per_cu(int kind, int mode);   // kind 0 compress, 1 grouped, 2 expand

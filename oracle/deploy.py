@@ -355,9 +355,35 @@ def controller(src: torch.Tensor, w: Mapping[str, object], precision: str,
     return meta
 
 
-def head(src: torch.Tensor, meta: torch.Tensor, w, out_dtype=torch.float16) -> torch.Tensor:
-    """FP32 reconstruction on FP16 coefficients, clamp [0,1], round to ``out_dtype``."""
-    out = M.reconstruct(src.float(), meta.float(), w["base"].float(), w["basis"].float())
+# FP16 value of 0.05 (0x2A66 = 0.04998779296875): the slope the quantized policies' head clamps with.
+H005 = float(np.float16(0.05))
+
+
+def coefficient_clamp_fp16(t: torch.Tensor) -> torch.Tensor:
+    """Clamped coefficient rounded to FP16, as the head of the quantized policies computes it.
+
+    c = a for |a| <= 2, else sign(a) * min(rne16((|a| - 2) * fp16(0.05) + 2), 2.5): one rounding
+    of an FP16 fused multiply-add (|a| - 2 is exact in FP16 for |a| > 2; the float64 product of two
+    11-bit significands and the sum with 2 are exact, so ``.half()`` is that single rounding).
+    +-inf -> +-2.5, NaN stays NaN.  The reference clamp (aeisu/reconstruction.py:15-17,
+    ``model.coefficient_clamp``) is FP32; this value is within half an FP16 ulp of c plus
+    (0.05 - fp16(0.05)) (|a| - 2) of it, and equal to it for |a| <= 2.
+    """
+    a = t.half().double()
+    m = a.abs()
+    soft = torch.clamp(((m - 2) * H005 + 2).half().double(), max=2.5)
+    c = torch.where(m <= 2, m, soft)
+    c = torch.where(torch.isnan(a), a, torch.copysign(c, a))
+    return c.float()
+
+
+def head(src: torch.Tensor, meta: torch.Tensor, w, out_dtype=torch.float16, clamp=None) -> torch.Tensor:
+    """FP32 reconstruction on FP16 coefficients, clamp [0,1], round to ``out_dtype``.
+
+    ``clamp``: the coefficient clamp (default the reference's FP32 ``coefficient_clamp``, which the
+    emulated deployments use; ``coefficient_clamp_fp16`` restates the quantized policies' GPU head).
+    """
+    out = M.reconstruct(src.float(), meta.float(), w["base"].float(), w["basis"].float(), clamp)
     return out.clamp(0, 1).to(out_dtype).float()
 
 

@@ -150,11 +150,13 @@ def coefficient_clamp(t: torch.Tensor) -> torch.Tensor:
     return torch.where(mag <= 2, t, torch.sign(t) * soft)
 
 
-def unpack_coefficients(meta: torch.Tensor) -> torch.Tensor:
+def unpack_coefficients(meta: torch.Tensor, clamp=None) -> torch.Tensor:
     """[B,64,h,w] parity-major -> clamped [B,16,2h,2w] (reconstruction.py:20-26).
 
     Channel 16*rho + k of packed cell (i, j) is coefficient k of the LR pixel
-    (2i + rho//2, 2j + rho%2).
+    (2i + rho//2, 2j + rho%2).  ``clamp`` replaces ``coefficient_clamp`` (the
+    quantized deployments' head rounds the clamped value to FP16, see
+    ``oracle.deploy.coefficient_clamp_fp16``).
     """
     bsz, ch, h, w = meta.shape
     if ch != 64:
@@ -162,11 +164,11 @@ def unpack_coefficients(meta: torch.Tensor) -> torch.Tensor:
     out = meta.new_empty(bsz, 16, 2 * h, 2 * w)
     for rho in range(4):
         out[:, :, rho >> 1::2, rho & 1::2] = meta[:, 16 * rho:16 * rho + 16]
-    return coefficient_clamp(out)
+    return (clamp or coefficient_clamp)(out)
 
 
 def reconstruct(src: torch.Tensor, meta: torch.Tensor, base: torch.Tensor,
-                basis: torch.Tensor) -> torch.Tensor:
+                basis: torch.Tensor, clamp=None) -> torch.Tensor:
     """Unclipped 2x RGB (reconstruction.py:29-83 with trim=0).
 
     out[2y+oy, 2x+ox, c] = sum_t (base[t,ph] + sum_k a_k(y,x) basis[t,k,ph])
@@ -175,7 +177,7 @@ def reconstruct(src: torch.Tensor, meta: torch.Tensor, base: torch.Tensor,
     bsz, _, h, w = src.shape
     if meta.shape != (bsz, 64, h // 2, w // 2):
         raise ValueError("Source/metadata geometry mismatch")
-    coeff = unpack_coefficients(meta)                       # [B,16,H,W]
+    coeff = unpack_coefficients(meta, clamp)                # [B,16,H,W]
     out = src.new_zeros(bsz, 3, 2 * h, 2 * w)
     for ph in range(4):
         acc = src.new_zeros(bsz, 3, h, w)

@@ -500,3 +500,72 @@ def test_area_bias_correction_within_weight_error_bound():
         assert corr.max() > 0, layer
     for layer in ("project", "refine", "tail"):
         assert np.array_equal(t[layer + ".bias_fp8"], t[layer + ".bias"]), layer
+
+
+# ------------------------------------------------------------------------------------------------
+# head of the quantized policies: the clamped coefficient rounded to FP16
+# ------------------------------------------------------------------------------------------------
+def _all_fp16_codes() -> torch.Tensor:
+    return torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
+
+
+def check_clamp_fp16(clamp) -> None:
+    """Properties that fix the FP16 clamp up to its rounding, over all 65536 FP16 codes:
+    identity (bit for bit, -0 included) for |a| <= 2; an FP16 value; within half an FP16 ulp plus
+    (0.05 - fp16(0.05)) (|a| - 2) of the reference's FP32 clamp; odd; non-decreasing in |a|;
+    +-inf -> +-2.5 and NaN -> NaN."""
+    a16 = _all_fp16_codes()
+    a = a16.float()
+    c = clamp(a)
+    finite = torch.isfinite(a)
+    small = finite & (a.abs() <= 2)
+    assert torch.equal(c[small].half().view(torch.int16), a16[small].view(torch.int16))
+    big = finite & (a.abs() > 2)
+    assert torch.equal(c[finite], c[finite].half().float())
+    ref = M.coefficient_clamp(a[big]).double()
+    ulp = (torch.nextafter(c[big].abs().half(), torch.tensor(float("inf"), dtype=torch.float16)).double()
+           - c[big].abs().double())
+    bound = ulp / 2 + (0.05 - D.H005) * (a[big].abs().double() - 2) + 1e-9
+    assert torch.all((c[big].double() - ref).abs() <= bound)
+    nonnan = ~torch.isnan(a)
+    assert torch.equal(clamp(-a[nonnan]), -c[nonnan])
+    pos = a[finite & (a > 0)].sort().values
+    cp = clamp(pos)
+    assert torch.all(cp[1:] >= cp[:-1])
+    assert clamp(torch.tensor([float("inf"), float("-inf")])).tolist() == [2.5, -2.5]
+    assert torch.isnan(clamp(torch.tensor([float("nan")]))).all()
+
+
+def test_coefficient_clamp_fp16_pins():
+    check_clamp_fp16(D.coefficient_clamp_fp16)
+
+
+@pytest.mark.parametrize("mistake", ["no_cap", "no_sign", "fp32_slope_unrounded", "no_select"])
+def test_planted_clamp_fp16_mistakes_are_caught(mistake):
+    def bad(t):
+        a = t.half().double()
+        m = a.abs()
+        if mistake == "fp32_slope_unrounded":
+            soft = torch.clamp((m - 2) * 0.05 + 2, max=2.5)          # not an FP16 value
+        else:
+            soft = ((m - 2) * D.H005 + 2).half().double()
+            if mistake != "no_cap":
+                soft = torch.clamp(soft, max=2.5)
+        c = soft if mistake == "no_select" else torch.where(m <= 2, m, soft)
+        c = torch.where(torch.isnan(a), a, c if mistake == "no_sign" else torch.copysign(c, a))
+        return c.float()
+    with pytest.raises(AssertionError):
+        check_clamp_fp16(bad)
+
+
+def test_head_fp16_clamp_stays_within_its_bound_of_the_reference_head(area_mixed):
+    """The quantized policies' head (FP16 clamped coefficients) against the reference FP32 clamp on a
+    scene frame whose coefficients are scaled so that most exceed the clamp: <= 0.1/255."""
+    from aeisu_amd import frames
+    src = frames.scene(48, 64, 4, shapes=6, texture=True)[None].half().float()
+    padded = F.pad(src, (16, 16, 16, 16), mode="replicate")
+    meta = (D.controller(padded, area_mixed, "mixed") * 3).half().float()
+    exact = D.head(padded, meta, area_mixed, out_dtype=torch.float32)
+    qc = D.head(padded, meta, area_mixed, out_dtype=torch.float32, clamp=D.coefficient_clamp_fp16)
+    err = (exact - qc).abs().max().item()
+    assert 0 < err <= 0.1 / 255

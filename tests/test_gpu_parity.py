@@ -89,6 +89,28 @@ def test_head_matches_oracle_reconstruction(fp16_model, area_state, scale):
     assert err < 1.5e-4
 
 
+@pytest.mark.parametrize("scale", [1.0, 3.0])
+def test_quantized_head_matches_oracle_reconstruction(mixed_model, area_state, scale):
+    """Head of the quantized policies (clamped coefficients rounded to FP16, one MFMA per row tile with
+    the FP32 base as accumulator input) on oracle coefficients: against the oracle's restatement of that
+    clamp (D.coefficient_clamp_fp16) within FP32 summation error, and against the reference's FP32 clamp
+    within 0.1/255."""
+    say(f"case: quantized-policy head vs oracle reconstruct, coefficient scale {scale}")
+    src = _frame(72, 104, 3)
+    padded = pad_frame(src[None])
+    meta = (M.controller(padded, area_state) * scale).half()
+    meta_nhwc = meta.permute(0, 2, 3, 1).contiguous().cuda()
+    got = mixed_model.head(src[None].cuda().contiguous(), meta_nhwc, out_dtype=torch.float32).cpu()
+    base, basis = area_state["base"], area_state["basis"]
+    ref16 = crop_output(M.reconstruct(padded, meta.float(), base, basis, D.coefficient_clamp_fp16).clamp(0, 1), 72, 104)
+    ref32 = crop_output(M.reconstruct(padded, meta.float(), base, basis).clamp(0, 1), 72, 104)
+    e16, e32 = (got - ref16).abs().max().item(), (got - ref32).abs().max().item()
+    say(f"  max|gpu - oracle (FP16 clamp)| = {e16:.3g}, max|gpu - oracle (FP32 clamp)| = {e32:.3g} ({e32 * 255:.3f}/255)")
+    # W = base + [K_hi | K_lo] . [c ; c]: base FP32, bank to ~2^-22, exact FP16 products, FP32 sums
+    assert e16 < 2e-5
+    assert e32 <= 0.1 / 255
+
+
 def test_head_phase_packing_exact(fp16_model, area_state):
     """Coefficients that select one parity/component at a time land on the right output pixels."""
     say("case: head parity packing")
