@@ -136,7 +136,12 @@ __device__ __forceinline__ void patch_store(const PatchRegs<LY>& r, unsigned cha
   }
 }
 
-// refine + tail for 16-pixel groups p*J .. p*J+J-1 of the tile (group q: packed row q/2, half q%2)
+// refine + tail for 16-pixel groups p*J .. p*J+J-1 of the tile (group q: packed row q/2, half q%2).
+// One producer wave per SIMD runs this, so nothing hides its LDS latency: the operands are pipelined
+// by hand, each weight fragment loaded one (tap, T) step ahead of its three MFMAs and each tap's
+// patch operands one tap ahead; the tail fragments are loaded once per call and shared by the J
+// groups (loaded per group, and waited for right before use, they left the producer at a third of
+// its issue rate).
 template <typename LY, bool QC>
 __device__ __forceinline__ void produce(const unsigned char* smem, const unsigned char* lds_patch,
                                         unsigned char* lds_meta, int p, int lane) {
@@ -157,34 +162,49 @@ __device__ __forceinline__ void produce(const unsigned char* smem, const unsigne
   for (int T = 0; T < 4; ++T)
 #pragma unroll
     for (int jj = 0; jj < J; ++jj) acc[T][jj] = f4{0.f, 0.f, 0.f, 0.f};
+  // refine fragment of step s = 4k + T is wf[(T * 9 + k) * 64 + lane]
+  h8 bcur[J], bnxt[J];
+#pragma unroll
+  for (int jj = 0; jj < J; ++jj) bcur[jj] = *reinterpret_cast<const h8*>(&patch[prow[jj]][pcol[jj] + n][8 * g]);
+  h8 anext = wf[lane];
 #pragma unroll
   for (int k = 0; k < 9; ++k) {
-    h8 b[J];
+    if (k < 8) {
 #pragma unroll
-    for (int jj = 0; jj < J; ++jj)
-      b[jj] = *reinterpret_cast<const h8*>(&patch[prow[jj] + k / 3][pcol[jj] + n + k % 3][8 * g]);
+      for (int jj = 0; jj < J; ++jj)
+        bnxt[jj] = *reinterpret_cast<const h8*>(&patch[prow[jj] + (k + 1) / 3][pcol[jj] + n + (k + 1) % 3][8 * g]);
+    }
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
-      const h8 a = wf[(T * 9 + k) * 64 + lane];
+      const h8 a = anext;
+      const int s = 4 * k + T + 1;
+      if (s < 36) anext = wf[((s & 3) * 9 + (s >> 2)) * 64 + lane];
 #pragma unroll
-      for (int jj = 0; jj < J; ++jj) acc[T][jj] = mfma_f16(a, b[jj], acc[T][jj]);
+      for (int jj = 0; jj < J; ++jj) acc[T][jj] = mfma_f16(a, bcur[jj], acc[T][jj]);
+    }
+    if (k < 8) {
+#pragma unroll
+      for (int jj = 0; jj < J; ++jj) bcur[jj] = bnxt[jj];
     }
   }
+  // refine epilogue -> the tail's B operands (refine channel order permuted on the host)
+  h8 bt[J][2];
 #pragma unroll
-  for (int jj = 0; jj < J; ++jj) {
-    h8 bt[2];
+  for (int jj = 0; jj < J; ++jj)
 #pragma unroll
     for (int T = 0; T < 4; ++T) {
       const f4 rb = bias[4 * T + g];                 // refine bias of channels 16T + 4g + r
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bt[T >> 1][(T & 1) * 4 + r] = (_Float16)leaky(acc[T][jj][r] + rb[r], 0.1f);
+      for (int r = 0; r < 4; ++r) bt[jj][T >> 1][(T & 1) * 4 + r] = (_Float16)leaky(acc[T][jj][r] + rb[r], 0.1f);
     }
-    _Float16* dst = reinterpret_cast<_Float16*>(lds_meta) + (prow[jj] * kFQW + pcol[jj] + n) * kFMPix + 4 * g;
 #pragma unroll
-    for (int T = 0; T < 4; ++T) {
-      f4 o = mfma_f16(wf[(kFRefineFrags + T * 2) * 64 + lane], bt[0], f4{0.f, 0.f, 0.f, 0.f});
-      o = mfma_f16(wf[(kFRefineFrags + T * 2 + 1) * 64 + lane], bt[1], o);
-      const f4 tb = bias[16 + 4 * T + g];            // FP16-rounded tail bias
+  for (int T = 0; T < 4; ++T) {
+    const h8 t0 = wf[(kFRefineFrags + T * 2) * 64 + lane], t1 = wf[(kFRefineFrags + T * 2 + 1) * 64 + lane];
+    const f4 tb = bias[16 + 4 * T + g];              // FP16-rounded tail bias
+#pragma unroll
+    for (int jj = 0; jj < J; ++jj) {
+      f4 o = mfma_f16(t0, bt[jj][0], f4{0.f, 0.f, 0.f, 0.f});
+      o = mfma_f16(t1, bt[jj][1], o);
       u2 w;
       w[0] = pack_h2(o[0] + tb[0], o[1] + tb[1]);
       w[1] = pack_h2(o[2] + tb[2], o[3] + tb[3]);
@@ -192,6 +212,7 @@ __device__ __forceinline__ void produce(const unsigned char* smem, const unsigne
         w[0] = coef_clamp_h16(w[0]);
         w[1] = coef_clamp_h16(w[1]);
       }
+      _Float16* dst = reinterpret_cast<_Float16*>(lds_meta) + (prow[jj] * kFQW + pcol[jj] + n) * kFMPix + 4 * g;
       *reinterpret_cast<u2*>(dst + 16 * T) = w;
     }
   }
