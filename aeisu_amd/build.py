@@ -51,8 +51,22 @@ def build_abi_smoke() -> Path:
     return ABI_SMOKE
 
 
+PROBE_SRC = ROOT / "tests" / "mfma_fp8_probe.hip"
+PROBE = ROOT / "tests" / "mfma_fp8_probe"
+
+
+def build_probe() -> Path:
+    """The GPU test program that measures the E4M3 MFMA's accumulation against the FP16 MFMA."""
+    cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", str(PROBE_SRC), "-o", str(PROBE)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"mfma_fp8_probe build failed:\n{res.stderr}")
+    return PROBE
+
+
 def build(jobs: int = 8) -> Path:
-    """Compile every source (always), link the shared library and the C++ ABI test program."""
+    """Compile every source (always), link the shared library and the C++ test programs."""
     BUILD.mkdir(exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objs = list(pool.map(_compile, sources()))
@@ -63,6 +77,7 @@ def build(jobs: int = 8) -> Path:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
     build_abi_smoke()
+    build_probe()
     return LIB
 
 
