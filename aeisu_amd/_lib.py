@@ -19,7 +19,7 @@ AEISU_ERR_ARTIFACT = -2
 AEISU_ERR_HIP = -3
 AEISU_ERR_STATE = -4
 AEISU_ERR_NONFINITE = -5
-PRECISION = {"fp16": 1, "mixed": 2, "int8": 3, "mixed-fp8mma": 4}
+PRECISION = {"fp16": 1, "mixed": 2, "int8": 3, "mixed-fp8mma": 4, "fp32": 5}
 LAYOUT_F16, LAYOUT_F32 = 0, 1
 FLAG_KEEP_INTERMEDIATES, FLAG_STAGE_TIMING, FLAG_NO_PAD, FLAG_UNFUSED, FLAG_BODY_TILE24 = 1, 2, 4, 8, 16
 FLAG_BODY_NO_EXCHANGE, FLAG_BODY_EXCHANGE_FALLBACK = 32, 64

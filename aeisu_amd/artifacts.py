@@ -133,10 +133,10 @@ def folded_to_fp16(payload) -> bytes:
             w, b = state[FOLDED_NAMES[layer] + ".weight"], state[FOLDED_NAMES[layer] + ".bias"]
         records += [(f"{layer}.weight_fp16", DT_F16, LAYOUT_OIHW, w.half().numpy()),
                     (f"{layer}.bias", DT_F32, LAYOUT_VECTOR, b.numpy()),
-                    (f"{layer}.prelu", DT_F32, LAYOUT_VECTOR, _prelu(layer, w.shape[0]))]
-        if layer == "project":
-            # kept at full precision: the FP16 policy splits it into FP16 hi + lo operands
-            records.append(("project.weight_fp32", DT_F32, LAYOUT_OIHW, w.numpy()))
+                    (f"{layer}.prelu", DT_F32, LAYOUT_VECTOR, _prelu(layer, w.shape[0])),
+                    # kept at full precision: the FP32 policy runs them as they are, and the FP16
+                    # policy splits the project weights into FP16 hi + lo operands
+                    (f"{layer}.weight_fp32", DT_F32, LAYOUT_OIHW, w.numpy())]
     basis = project_basis(state["basis_raw"], scale).numpy()
     _common(records, _analysis_vector(lambda k: state[k].numpy()), state["base_kernel"].numpy(), basis)
     return write(records)

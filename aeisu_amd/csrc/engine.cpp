@@ -261,20 +261,23 @@ struct LayerDev {
 // ------------------------------------------------------------------------------------------------
 constexpr int kStageEvents = AEISU_STAGE_COUNT;  // 7 boundaries per frame (start + 6 stage ends)
 constexpr int kMaxTimedFrames = 4096;
-constexpr int kModes = 4;
+constexpr int kModes = 5;
+constexpr int kModeFp32 = 4;
 
-// Kernel mode of a precision: 0 FP16, 1 E4M3 on the FP8 MFMA, 2 INT8, 3 E4M3 values on the FP16 MFMA.
+// Kernel mode of a precision: 0 FP16, 1 E4M3 on the FP8 MFMA, 2 INT8, 3 E4M3 values on the FP16 MFMA,
+// 4 FP32 (per-layer FP32 kernels, k_fp32.hip).
 static int mode_of(int precision) {
   switch (precision) {
     case AEISU_PRECISION_FP16: return 0;
     case AEISU_PRECISION_MIXED_FP8MMA: return 1;
     case AEISU_PRECISION_INT8: return 2;
     case AEISU_PRECISION_MIXED: return 3;
+    case AEISU_PRECISION_FP32: return kModeFp32;
     default: fail(AEISU_ERR_INVALID_ARGUMENT, "unknown precision");
   }
 }
 static const char* precision_name(int mode) {
-  static const char* names[kModes] = {"FP16", "FP8-E4M3 on the FP8 MFMA", "INT8/FP16", "FP8/FP16-Mixed"};
+  static const char* names[kModes] = {"FP16", "FP8-E4M3 on the FP8 MFMA", "INT8/FP16", "FP8/FP16-Mixed", "FP32"};
   return names[mode];
 }
 
@@ -288,6 +291,7 @@ struct ModeWeights {
   DeviceBuffer compress_rgb;       // INT8 compress weights in the frame-input fused body's K order
   DeviceBuffer tail_bias;
   DeviceBuffer body_consts;        // epilogue constants of the fused body (kBodyConsts floats)
+  DeviceBuffer fp32;               // FP32 policy: the whole weight image (kernels.hpp kF32*)
 
   // every device buffer, for commit() and byte accounting
   template <typename Fn>
@@ -301,6 +305,7 @@ struct ModeWeights {
     fn(compress_rgb);
     fn(tail_bias);
     fn(body_consts);
+    fn(fp32);
   }
   size_t bytes() const {
     size_t n = 0;
@@ -335,6 +340,8 @@ struct Model {
 struct Geometry {
   int batch = 0, H = 0, W = 0, Hp = 0, Wp = 0, py = 0, px = 0, Hq = 0, Wq = 0, Hl = 0, Wl = 0;
   int in_fp32 = 0, out_fp32 = 0;
+  int act_bytes = 2;               // bytes per skip / work / coefficient element (FP32 policy: 4)
+  int low_bytes = 2;               // bytes per low-resolution activation (FP16 2, byte policies 1, FP32 4)
   int qclamp = 0;                  // head of the quantized policies: clamped coefficients in FP16
   unsigned flags = 0;
   bool fused = false;              // fused body kernel, and refine + tail + head in one kernel
@@ -352,9 +359,10 @@ struct Geometry {
   size_t packed() const { return size_t(batch) * Hq * Wq; }
   size_t lowpx() const { return size_t(batch) * Hl * Wl; }
   // device scratch of the configuration (bytes): skip, work, meta, low activations
-  size_t skip_bytes() const { return fused_rgb ? 0 : packed() * 32 * 2; }
-  size_t work_bytes() const { return packed() * 32 * 2; }
-  size_t meta_bytes() const { return fused ? 0 : packed() * 64 * 2; }
+  size_t skip_bytes() const { return fused_rgb ? 0 : packed() * 32 * act_bytes; }
+  size_t work_bytes() const { return packed() * 32 * act_bytes; }
+  size_t meta_bytes() const { return fused ? 0 : packed() * 64 * act_bytes; }
+  size_t low_layer_bytes() const { return lowpx() * 64 * low_bytes; }
   // compress exchange: the cores' compress codes (64 bytes per low pixel) and one counter per tile
   size_t xbuf_bytes() const { return body_xc_tile ? lowpx() * 64 : 0; }
   size_t xflag_bytes() const {
@@ -437,6 +445,41 @@ static void require_prelu(const Artifact& a, const std::string& layer, uint32_t 
 
 static std::vector<float> as_f32_vector(const TensorView& t) { return std::vector<float>(t.f32(), t.f32() + t.count()); }
 
+// FP32 policy: every layer's FP32 weights (<layer>.weight_fp32, written by the folded-checkpoint
+// converter) re-laid [tap][ci][co] into one image (kernels.hpp kF32*).
+static void pack_fp32(ModeWeights& rt, const Artifact& a, const float* base, const float* basis) {
+  std::vector<float> img(kF32Floats, 0.f);
+  auto w32 = [&](const std::string& l, uint32_t cout, uint32_t cin, uint32_t ks) {
+    if (!a.has(l + ".weight_fp32"))
+      fail(AEISU_ERR_ARTIFACT, "the FP32 policy needs " + l + ".weight_fp32 (convert a folded FP32 checkpoint)");
+    return a.need(l + ".weight_fp32", kF32, {cout, cin, ks, ks}).f32();
+  };
+  auto layer = [&](const std::string& l, uint32_t cout, uint32_t cin, uint32_t ks, int off, float slope) {
+    const float* w = w32(l, cout, cin, ks);
+    require_prelu(a, l, cout, slope);
+    const float* b = a.need(l + ".bias", kF32, {cout}).f32();
+    for (uint32_t o = 0; o < cout; ++o) {
+      for (uint32_t i = 0; i < cin; ++i)
+        for (uint32_t t = 0; t < ks * ks; ++t) {
+          const float v = w[(size_t(o) * cin + i) * ks * ks + t];
+          if (!std::isfinite(v)) fail(AEISU_ERR_ARTIFACT, "nonfinite weight in " + l);
+          img[off + (size_t(t) * cin + i) * cout + o] = v;         // [tap][ci][co]
+        }
+      img[off + size_t(ks * ks) * cin * cout + o] = b[o];
+    }
+  };
+  layer("project", 32, 32, 1, kF32Project, 0.1f);
+  layer("compress", 64, 128, 1, kF32Compress, 0.1f);
+  for (int l = 0; l < 4; ++l) layer("bottleneck" + std::to_string(l), 64, 32, 3, kF32Grouped + l * kF32GroupedStride, 0.1f);
+  layer("expand", 128, 64, 1, kF32Expand, 0.1f);
+  layer("refine", 64, 32, 3, kF32Refine, 0.1f);
+  layer("tail", 64, 64, 1, kF32Tail, 1.0f);
+  for (int i = 0; i < 100; ++i) img[kF32Base + i] = base[i];
+  for (int i = 0; i < 1600; ++i) img[kF32Basis + i] = basis[i];
+  for (int i = 0; i < 24; ++i) img[kF32Analysis + i] = rt.analysis[i];
+  rt.fp32.upload(img);
+}
+
 static void pack_weights(ModeWeights& rt, const Artifact& a) {
   // --- shared tensors and contracts (SrcPyrModel.cpp:355-422)
   const TensorView& stencil = a.need("analysis_stencil", kF32, {24});
@@ -461,12 +504,17 @@ static void pack_weights(ModeWeights& rt, const Artifact& a) {
   const TensorView& guards = a.need("precision_guards", kF32, {2});
   for (int i = 0; i < 2; ++i)
     if (guards.f32()[i] != 0.f && guards.f32()[i] != 1.f) fail(AEISU_ERR_ARTIFACT, "Invalid adaptive precision policy");
-  if (rt.mode != 0) {
+  if (rt.mode != 0 && rt.mode != kModeFp32) {
     const TensorView& s = a.need("activation_scales", kF32, {10});
     for (int i = 0; i < 10; ++i) {
       rt.act[i] = s.f32()[i];
       if (!std::isfinite(rt.act[i]) || rt.act[i] <= 0) fail(AEISU_ERR_ARTIFACT, "invalid activation scale");
     }
+  }
+
+  if (rt.mode == kModeFp32) {
+    pack_fp32(rt, a, base.f32(), basis.f32());
+    return;
   }
 
   // --- FP16 layers used by every policy: project, refine, tail
@@ -756,6 +804,14 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
   g.in_fp32 = in_layout == AEISU_LAYOUT_NCHW_F32;
   g.out_fp32 = out_layout == AEISU_LAYOUT_NCHW_F32;
   g.flags = flags;
+  g.cus = cus;
+  if (mode == kModeFp32) {
+    // per-layer FP32 kernels, one thread per pixel (no persistent grids, no fused variants)
+    g.act_bytes = g.low_bytes = 4;
+    g.nlow = (flags & AEISU_FLAG_KEEP_INTERMEDIATES) ? 5 : 2;
+    return g;
+  }
+  g.low_bytes = mode == 0 ? 2 : 1;
   g.fused = !(flags & (AEISU_FLAG_KEEP_INTERMEDIATES | AEISU_FLAG_UNFUSED));
   // the skip tensor only exists in device memory where the project kernel runs
   g.fused_rgb = g.fused && mode != 0;
@@ -916,8 +972,28 @@ static void enqueue_head(const ModeWeights& w, const Geometry& g, const Scratch&
                         g.py, g.px, g.batch, sc.nonfinite, g.grid.head, s), "head launch");
 }
 
+// FP32 policy: project, compress, 4 grouped, expand, refine + tail, head; events 0..6 as the per-layer path
+static void enqueue_fp32(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in, void* d_out,
+                         hipStream_t s, hipEvent_t* ev) {
+  if (ev) check_hip(hipEventRecord(ev[0], s), "hipEventRecord");
+  float* lows[5];
+  for (int i = 0; i < 5; ++i) lows[i] = static_cast<float*>(sc.low[i]);
+  check_hip(launch_f32_controller(g.in_fp32, d_in, w.fp32.as<float>(), static_cast<float*>(sc.skip), lows[0], lows[1],
+                                  g.nlow == 5 ? lows : nullptr, static_cast<float*>(sc.work), static_cast<float*>(sc.meta),
+                                  g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, s, ev),
+            "FP32 controller launch");
+  check_hip(launch_f32_head(g.in_fp32, g.out_fp32, d_in, static_cast<const float*>(sc.meta), w.fp32.as<float>(), d_out,
+                            g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, s),
+            "FP32 head launch");
+  if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
+}
+
 static void enqueue_frame(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in, void* d_out,
                           hipStream_t s, hipEvent_t* ev) {
+  if (w.mode == kModeFp32) {
+    enqueue_fp32(w, g, sc, d_in, d_out, s, ev);
+    return;
+  }
   if (!g.fused) {
     enqueue_controller(w, g, sc, d_in, sc.meta, s, ev);
     enqueue_head(w, g, sc, d_in, sc.meta, d_out, s);
@@ -943,7 +1019,7 @@ static std::string startup_report(const Runtime& rt) {
     << " body=" << (g.fused ? (g.fused_rgb ? "fused-analysis-project-compress-4x-grouped-expand"
                                            : "project+fused-compress-4x-grouped-expand")
                             : "per-layer-kernels")
-    << " body_mfma=" << (rt.mode == 0 ? "f16" : rt.mode == 1 ? "fp8" : rt.mode == 2 ? "i8" : "f16-on-e4m3-values")
+    << " body_mfma=" << (rt.mode == 0 ? "f16" : rt.mode == 1 ? "fp8" : rt.mode == 2 ? "i8" : rt.mode == 3 ? "f16-on-e4m3-values" : "none-fp32-fma")
     << " head=" << (g.fused ? "fused-refine-tail-reconstruction" : "refine-tail+reconstruction")
     << " source=" << g.W << 'x' << g.H << " batch=" << g.batch << " padded=" << g.Wp << 'x' << g.Hp
     << " packed=" << g.Wq << 'x' << g.Hq << " low=" << g.Wl << 'x' << g.Hl << " source_pad=" << g.px << ','
@@ -966,7 +1042,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   rt.skip.alloc(g.skip_bytes());
   rt.work.alloc(g.work_bytes());
   rt.meta.alloc(g.meta_bytes());
-  for (int i = 0; i < 5; ++i) rt.low[i].alloc(i < g.nlow ? g.lowpx() * 64 * (mode == 0 ? 2 : 1) : 0);
+  for (int i = 0; i < 5; ++i) rt.low[i].alloc(i < g.nlow ? g.low_layer_bytes() : 0);
   rt.nonfinite.alloc(4);
   check_hip(hipMemset(rt.nonfinite.ptr, 0, 4), "hipMemset(flag)");
   rt.xbuf.alloc(g.xbuf_bytes());
@@ -1000,6 +1076,9 @@ static void require_configured(const Runtime& rt) {
 // each 256-byte aligned.
 static void enqueue_noalloc(const Runtime& rt, int batch, int height, int width, int in_layout, int out_layout,
                             const void* d_in, void* d_out, hipStream_t s) {
+  if (rt.mode == kModeFp32)
+    fail(AEISU_ERR_STATE, "the allocation-free entry point runs the fused path; the FP32 policy runs per-layer "
+                          "kernels on FP32 activations (use aeisu_upscale_async)");
   Geometry g = make_geometry(rt.mode, rt.w->project_precise, rt.model->cu_count, batch, height, width, in_layout,
                              out_layout, 0);
   g.body_xc_tile = 0;                              // the exchange needs its own zeroed counters
@@ -1239,9 +1318,9 @@ size_t aeisu_intermediate_bytes(const aeisu_runtime* h, int which) {
   if (!h || !h->impl || !h->impl->configured) return 0;
   const Runtime& rt = *h->impl;
   const size_t packed = rt.g.packed(), lowpx = rt.g.lowpx();
-  if (which == AEISU_BUF_SKIP || which == AEISU_BUF_WORK) return packed * 64;
-  if (which == AEISU_BUF_META) return packed * 128;
-  if (which >= AEISU_BUF_LOW0 && which <= AEISU_BUF_LOW4) return lowpx * 64 * (rt.mode == 0 ? 2 : 1);
+  if (which == AEISU_BUF_SKIP || which == AEISU_BUF_WORK) return packed * 32 * rt.g.act_bytes;
+  if (which == AEISU_BUF_META) return packed * 64 * rt.g.act_bytes;
+  if (which >= AEISU_BUF_LOW0 && which <= AEISU_BUF_LOW4) return lowpx * 64 * rt.g.low_bytes;
   return 0;
 }
 

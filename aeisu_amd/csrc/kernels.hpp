@@ -100,6 +100,33 @@ hipError_t launch_fused_tail_head(int in_fp32, int out_fp32, int qclamp, const v
                                   void* out, int H, int W, int Hq, int Wq, int py, int px, int batch,
                                   unsigned* nonfinite, int grid, hipStream_t stream);
 
+// FP32 policy (k_fp32.hip): per-layer kernels on FP32 NHWC activations.  Weight image (floats),
+// every layer [tap][ci][co] (co fastest) followed by its bias:
+//   project  W[32 feature channel f*4+phase][32] b[32]; compress W[128 skip channel c*4+phase][64] b[64];
+//   bottleneck l: W[9][32 group input][64] b[64] (output 32g+o reads group g's inputs);
+//   expand W[64][128] b[128] (output c*4+phase); refine W[9][32][64] b[64]; tail W[64][64] b[64];
+//   then adaptive_base [25][4], adaptive_basis [25][16][4], the 24 analysis constants.
+constexpr int kF32Project = 0;
+constexpr int kF32Compress = kF32Project + 32 * 32 + 32;
+constexpr int kF32GroupedStride = 9 * 32 * 64 + 64;
+constexpr int kF32Grouped = kF32Compress + 128 * 64 + 64;
+constexpr int kF32Expand = kF32Grouped + 4 * kF32GroupedStride;
+constexpr int kF32Refine = kF32Expand + 64 * 128 + 128;
+constexpr int kF32Tail = kF32Refine + 9 * 32 * 64 + 64;
+constexpr int kF32Base = kF32Tail + 64 * 64 + 64;
+constexpr int kF32Basis = kF32Base + 25 * 4;
+constexpr int kF32Analysis = kF32Basis + 25 * 16 * 4;
+constexpr int kF32Floats = kF32Analysis + 24;
+// project, compress, the four grouped layers, expand, refine + tail (events 1..5 after each stage
+// when ev is not null); lows: the five layer outputs when every layer is kept, else null (ping-pong
+// between low0 and low1)
+hipError_t launch_f32_controller(int in_fp32, const void* src, const float* wimg, float* skip, float* low0, float* low1,
+                                 float* const* lows, float* work, float* meta, int H, int W, int Hq, int Wq, int py, int px,
+                                 int batch, hipStream_t stream, hipEvent_t* ev);
+hipError_t launch_f32_head(int in_fp32, int out_fp32, const void* src, const float* meta, const float* wimg, void* out,
+                           int H, int W, int Hq, int Wq, int py, int px, int batch, unsigned* nonfinite,
+                           hipStream_t stream);
+
 // Resident blocks per CU (occupancy), used to size the persistent grids.
 int head_blocks_per_cu(int in_fp32, int out_fp32, int qclamp);
 int project_blocks_per_cu(int in_fp32, int precise);

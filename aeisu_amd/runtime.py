@@ -229,11 +229,12 @@ def load_model(path, device: str = "cuda", precision: Optional[str] = None) -> U
     """Load a released weight file (folded .pt, SPYR8F8 .bin or INT8 .pt) onto the GPU.
 
     Mirrors aeisu/runtime.py:45-56.  ``precision`` defaults to the file's
-    natural policy; an FP8 artifact can also run at "fp16" (its FP16 weights).
+    natural policy; an FP8 artifact can also run at "fp16" (its FP16 weights), a folded FP32
+    checkpoint also at "fp32" (FP32 activations and arithmetic: the reference's PyTorch path).
     """
     blob, natural = load_blob(Path(path))
     precision = precision or natural
-    allowed = {"fp16": {"fp16"}, "mixed": {"mixed", "mixed-fp8mma", "fp16"}, "int8": {"int8"}}[natural]
+    allowed = {"fp16": {"fp16", "fp32"}, "mixed": {"mixed", "mixed-fp8mma", "fp16"}, "int8": {"int8"}}[natural]
     if precision not in allowed:
         raise ValueError(f"{Path(path).name} provides {sorted(allowed)}, not {precision!r}")
     return Upscaler(blob, precision, device)

@@ -34,7 +34,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
-MFMA_PEAK = {"fp16": 2.5e15, "fp8": 5.0e15, "int8": 5.0e15}
+MFMA_PEAK = {"fp16": 2.5e15, "fp8": 5.0e15, "int8": 5.0e15, "fp32": 157.3e12}   # dense; fp32: MI355X FP32 peak
 CTRL_MAC_FP16 = 256 + 4608 + 1024        # project + refine + tail, per LR pixel (paper tex:352-359)
 CTRL_MAC_LOW = 512 + 4608 + 512          # compress + 4 bottlenecks + expand
 WORKLOADS = {
@@ -124,7 +124,7 @@ def main():
                     help="input frame size override for resolution sweeps (the headline value is config 2)")
     ap.add_argument("--batch", type=int, default=None, help="batch override for sweeps")
     ap.add_argument("--precision", default=None,
-                    help="precision policy override the weight file allows (fp16, mixed, mixed-fp8mma, int8)")
+                    help="precision policy override the weight file allows (fp16, fp32, mixed, mixed-fp8mma, int8)")
     ap.add_argument("--clock-warmup", type=float, default=0.5, metavar="S",
                     help="seconds of untimed frames before the warm-up steps, so the timed frames run at the "
                          "clocks a sustained load reaches")
@@ -222,10 +222,12 @@ def main():
     synth_flops = 2.0 * lr_px * 16 * 100                      # head filter synthesis (MFMA)
     # MFMA the low-precision layers run on: the Mixed policy feeds E4M3 values to the FP16 MFMA
     # (exact products, FP32 accumulation), INT8 uses the i8 MFMA
-    low_kind = {"fp16": "fp16", "mixed": "fp16", "mixed-fp8mma": "fp8", "int8": "int8"}[wl["precision"]]
+    low_kind = {"fp16": "fp16", "mixed": "fp16", "mixed-fp8mma": "fp8", "int8": "int8", "fp32": "fp32"}[wl["precision"]]
+    # the FP32 policy runs FP32 FMAs everywhere (per-layer kernels, no fused variants)
+    hi_kind = "fp32" if wl["precision"] == "fp32" else "fp16"
     ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
     ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
-    fused = not args.unfused                                  # fused body and fused refine+tail+head kernels
+    fused = not args.unfused and wl["precision"] != "fp32"   # fused body and fused refine+tail+head kernels
     traffic = {} if sweep else measured_traffic(args.config)   # the profiles cover configs 1-4 as defined
     kernels = {}
     proj_bytes = lr_px * 3 * s_io + packed_px * 32 * 2        # RGB in + FP16 skip out
@@ -279,12 +281,13 @@ def main():
         kernels["head"] = {"bound": "hbm", "achieved": head_bytes / head_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                            "frac": head_bytes / head_s / HBM_PEAK, "ms": stages["head"],
                            "algorithmic_bytes": head_bytes, "traffic": traffic.get("head")}
-        kernels["refine_tail"] = {"bound": "mfma", "achieved": refine_flops / refine_s / 1e12,
-                                  "peak": MFMA_PEAK["fp16"] / 1e12, "unit": "TFLOP/s",
-                                  "frac": refine_flops / refine_s / MFMA_PEAK["fp16"], "ms": stages["refine_tail"],
+        kernels["refine_tail"] = {"bound": "mfma" if hi_kind == "fp16" else "valu",
+                                  "achieved": refine_flops / refine_s / 1e12,
+                                  "peak": MFMA_PEAK[hi_kind] / 1e12, "unit": "TFLOP/s",
+                                  "frac": refine_flops / refine_s / MFMA_PEAK[hi_kind], "ms": stages["refine_tail"],
                                   "algorithmic_flops": refine_flops, "traffic": traffic.get("refine_tail")}
         ctrl_ms = sum(stages[k] for k in ("project", "compress", "bottleneck", "expand", "refine_tail"))
-    ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK["fp16"] + ctrl_flops_low / MFMA_PEAK[low_kind]
+    ctrl_ideal_s = ctrl_flops16 / MFMA_PEAK[hi_kind] + ctrl_flops_low / MFMA_PEAK[low_kind]
     dominant = max(kernels, key=lambda k: kernels[k]["ms"])
     roof = {k: v for k, v in kernels[dominant].items()
             if k in ("bound", "achieved", "peak", "unit", "frac", "traffic", "limiter")}
@@ -317,7 +320,7 @@ def main():
         "ms_per_step": round(ms_per_step, 5), "ms_per_frame": round(ms_per_step / B, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"fp16": "fp16", "mixed": "fp8-e4m3/fp16", "mixed-fp8mma": "fp8-e4m3/fp16",
-                  "int8": "int8/fp16"}[wl["precision"]],
+                  "int8": "int8/fp16", "fp32": "fp32"}[wl["precision"]],
         "data": f"synthetic (aeisu_amd.frames config {args.config}, {args.pool} resident frames)",
         "config": {"workload": wl["name"] + (" (sweep override)" if sweep else ""), "config_id": args.config,
                    "batch": B, "input": [3, H, W],

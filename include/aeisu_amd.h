@@ -41,6 +41,11 @@ extern "C" {
                                           accumulation rounded inside the unit): up to 3.1/255 from the
                                           Mixed emulation, outside the 2/255 bound of MIXED; for
                                           comparison only */
+#define AEISU_PRECISION_FP32 5  /* FP32 activations and FP32 arithmetic in every layer and the head
+                                   (per-layer kernels): the reference's PyTorch FP32 path
+                                   (aeisu/model.py, aeisu/runtime.py).  Needs FP32 weights for every
+                                   layer (<layer>.weight_fp32, written by the folded-checkpoint
+                                   converter); not served by aeisu_upscale_noalloc */
 
 /* frame buffer layouts: planar RGB, batch-major [B][3][H][W] */
 #define AEISU_LAYOUT_NCHW_F16 0
@@ -92,8 +97,9 @@ typedef struct aeisu_runtime aeisu_runtime;
  * (SrcPyrCudaRuntime.cu:5380-5383, 2924-3170; SrcPyrModel.cpp:243-470).
  * The artifact is SPYR8F8 (SrcPyrModel.cpp:37-81); FP16 needs the *.weight_fp16
  * tensors, MIXED the *.weight_fp8 / weight_scale / bias_fp8 / activation_scales
- * tensors, INT8 the *.weight_i8 / int8_factor tensors (data type 6).  `precision`
- * is the policy the runtime runs until aeisu_configure names another one. */
+ * tensors, INT8 the *.weight_i8 / int8_factor tensors (data type 6), FP32 the *.weight_fp32
+ * tensors of every layer.  `precision` is the policy the runtime runs until aeisu_configure names
+ * another one. */
 int aeisu_create_from_file(const char* path, int precision, aeisu_runtime** out);
 int aeisu_create_from_memory(const void* data, size_t size, int precision, aeisu_runtime** out);
 

@@ -54,7 +54,8 @@ def test_binding_constants_match_header():
                  "AEISU_ERR_NONFINITE"):
         assert getattr(L, name) == h[name], name
     assert L.PRECISION == {"fp16": h["AEISU_PRECISION_FP16"], "mixed": h["AEISU_PRECISION_MIXED"],
-                           "int8": h["AEISU_PRECISION_INT8"], "mixed-fp8mma": h["AEISU_PRECISION_MIXED_FP8MMA"]}
+                           "int8": h["AEISU_PRECISION_INT8"], "mixed-fp8mma": h["AEISU_PRECISION_MIXED_FP8MMA"],
+                           "fp32": h["AEISU_PRECISION_FP32"]}
     flags = {k[len("AEISU_"):]: v for k, v in h.items() if k.startswith("AEISU_FLAG_")}
     assert len(flags) >= 5
     for name, value in flags.items():
@@ -97,11 +98,21 @@ def blobs():
 
 
 @pytest.mark.parametrize("prec,src", [("fp16", "fp16"), ("mixed", "mixed"), ("int8", "int8"), ("fp16", "mixed"),
-                                      ("mixed-fp8mma", "mixed")])
+                                      ("mixed-fp8mma", "mixed"), ("fp32", "fp16")])
 def test_valid_artifacts_pass_validation(blobs, prec, src):
     rc, msg = _create(blobs[src], prec)
     # a CPU-only box fails only at the first HIP call, after validation succeeded
     assert rc == L.AEISU_OK or (rc == L.AEISU_ERR_HIP and "hip" in msg.lower()), msg
+
+
+def test_fp32_policy_needs_fp32_weights(blobs):
+    """FP32 runs every layer's FP32 weights: an FP8 artifact (no *.weight_fp32) is rejected during
+    validation, before any HIP call, naming the first missing tensor."""
+    rc, msg = _create(blobs["mixed"], "fp32")
+    assert rc == L.AEISU_ERR_ARTIFACT and "project.weight_fp32" in msg, msg
+    no_refine = _rewrite(blobs["fp16"], lambda name, a: None if name == "refine.weight_fp32" else a)
+    rc, msg = _create(no_refine, "fp32")
+    assert rc == L.AEISU_ERR_ARTIFACT and "refine.weight_fp32" in msg, msg
 
 
 def test_writer_round_trip_with_oracle_reader(blobs):
@@ -110,6 +121,10 @@ def test_writer_round_trip_with_oracle_reader(blobs):
     t = art["tensors"]
     assert np.array_equal(t["project.weight_fp16"], state["project_540.weight"].half().numpy())
     assert np.array_equal(t["project.weight_fp32"], state["project_540.weight"].numpy())
+    # every layer's FP32 weights travel for the FP32 policy
+    assert np.array_equal(t["expand.weight_fp32"], state["expand_270.weight"].numpy())
+    assert np.array_equal(t["bottleneck1.weight_fp32"], torch.cat((state["bottleneck_270_a2.weight"],
+                                                                   state["bottleneck_270_b2.weight"])).numpy())
     assert np.array_equal(t["bottleneck3.bias"], torch.cat((state["bottleneck_270_a4.bias"],
                                                              state["bottleneck_270_b4.bias"])).numpy())
     assert np.array_equal(t["adaptive_basis"], state["basis"].numpy())
