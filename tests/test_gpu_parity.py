@@ -2,7 +2,8 @@
 
 Tolerances:
 * FP16 policy vs the reference FP32 model: <= 1e-3 max-abs on [0,1] RGB
-  (white-noise goldens: 3e-3, the FP16 storage bound; see that test).
+  (white-noise goldens: 3e-3, the FP16 storage bound; see that test; the FP32
+  policy holds them to 2e-5, tests/test_gpu_fp32.py).
 * Mixed FP8 / INT8 policies vs their CPU emulation: <= 2/255 max-abs and
   output PSNR within 0.05 dB against a target.
 * Phase packing / indexing: exact (checked through the head on synthetic
@@ -173,7 +174,9 @@ def test_fp16_end_to_end_vs_reference_golden(fp16_model, area_state, R, case):
     from the FP32 reference, so the GPU is held to the emulation tightly and to
     the reference with the FP16-storage bound 3e-3 (the reference's own FP16
     adapter measures 3.19e-3 on its random probe,
-    research/runtime/pytorch/aeisu_fp16_1080/protocol.json).
+    research/runtime/pytorch/aeisu_fp16_1080/protocol.json).  The FP32 policy
+    meets 1e-3 on these frames (3e-6 measured, tests/test_gpu_fp32.py); the FP16
+    policy meets it on the natural-image classes (config 1 recipe, below).
     """
     g = golden("area")
     src = torch.from_numpy(g[f"{case}_input"])
