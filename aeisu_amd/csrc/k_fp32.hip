@@ -104,7 +104,9 @@ __global__ __launch_bounds__(kF32Threads) void f32_compress_kernel(const float* 
                     leaky01(acc[co + 2] + wc[8194 + co]), leaky01(acc[co + 3] + wc[8195 + co]));
 }
 
-// ---- grouped 3x3 (2 groups of 32 -> 32, zero padding) + LeakyReLU: one low pixel per thread -------
+// ---- grouped 3x3 (2 groups of 32 -> 32, zero padding) + LeakyReLU: one low pixel and group per
+// thread; blockIdx.y is the group, so the weight rows stay block-uniform (scalar loads) and a 1080p
+// layer runs four waves per SIMD instead of two
 __global__ __launch_bounds__(kF32Threads) void f32_grouped_kernel(const float* __restrict__ in, const float* __restrict__ wl,
                                                                   float* __restrict__ out, int Hl, int Wl, int batch) {
   const long idx = (long)blockIdx.x * kF32Threads + threadIdx.x;
@@ -112,7 +114,8 @@ __global__ __launch_bounds__(kF32Threads) void f32_grouped_kernel(const float* _
   const int b = (int)(idx / ((long)Hl * Wl));
   const int rem = (int)(idx - (long)b * Hl * Wl);
   const int ly = rem / Wl, lx = rem - ly * Wl;
-  for (int grp = 0; grp < 2; ++grp) {
+  const int grp = blockIdx.y;
+  {
     float acc[32];
 #pragma unroll
     for (int o = 0; o < 32; ++o) acc[o] = 0.f;
@@ -215,20 +218,24 @@ __global__ __launch_bounds__(kF32Threads) void f32_refine_tail_kernel(const floa
       }
     }
   }
-  float t[64];
 #pragma unroll
-  for (int co = 0; co < 64; ++co) t[co] = 0.f;
-#pragma unroll
-  for (int ci = 0; ci < 64; ++ci) {
-    const float x = leaky01(r[ci] + wr[18432 + ci]);
-#pragma unroll
-    for (int co = 0; co < 64; ++co) t[co] = fmaf(x, wt[ci * 64 + co], t[co]);
-  }
+  for (int ci = 0; ci < 64; ++ci) r[ci] = leaky01(r[ci] + wr[18432 + ci]);
+  // the tail in two halves of 32 outputs: 64 + 32 accumulators stay within 128 VGPRs (four waves
+  // per SIMD; all 64 + 64 took 129)
   float* out = meta + (size_t)idx * 64;
+  for (int h = 0; h < 64; h += 32) {
+    float t[32];
 #pragma unroll
-  for (int co = 0; co < 64; co += 4)
-    *reinterpret_cast<float4*>(out + co) = make_float4(t[co] + wt[4096 + co], t[co + 1] + wt[4097 + co],
-                                                       t[co + 2] + wt[4098 + co], t[co + 3] + wt[4099 + co]);
+    for (int co = 0; co < 32; ++co) t[co] = 0.f;
+#pragma unroll
+    for (int ci = 0; ci < 64; ++ci)
+#pragma unroll
+      for (int co = 0; co < 32; ++co) t[co] = fmaf(r[ci], wt[ci * 64 + h + co], t[co]);
+#pragma unroll
+    for (int co = 0; co < 32; co += 4)
+      *reinterpret_cast<float4*>(out + h + co) = make_float4(t[co] + wt[4096 + h + co], t[co + 1] + wt[4097 + h + co],
+                                                             t[co + 2] + wt[4098 + h + co], t[co + 3] + wt[4099 + h + co]);
+  }
 }
 
 // ---- head: clamp, polyphase filter synthesis, 5x5 application, clip: one LR pixel per thread -------
@@ -335,7 +342,7 @@ hipError_t launch_f32_controller(int in_fp32, const void* src, const float* wimg
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (ev && (e = hipEventRecord(ev[2], stream)) != hipSuccess) return e;
   for (int l = 0; l < 4; ++l) {
-    hipLaunchKernelGGL(f32_grouped_kernel, dim3(f32_grid(lowpx)), dim3(kF32Threads), 0, stream, (const float*)dst[l],
+    hipLaunchKernelGGL(f32_grouped_kernel, dim3(f32_grid(lowpx), 2), dim3(kF32Threads), 0, stream, (const float*)dst[l],
                        wimg + kF32Grouped + l * kF32GroupedStride, dst[l + 1], Hl, Wl, batch);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
