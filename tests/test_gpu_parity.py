@@ -370,6 +370,37 @@ def _policy_case(model, weights, precision, h, w, seed):
     return src16, got, ref, rec
 
 
+@pytest.mark.parametrize("h,w,b", [(1, 1, 1), (2, 3, 1), (1, 9, 1), (7, 1, 1), (5, 5, 1), (33, 65, 2)])
+def test_tiny_and_ragged_frames(fp16_model, mixed_model, int8_model, area_state, R, h, w, b):
+    """Frames of one pixel, one row or one column, and ragged sizes: the runtime pads them to the
+    align32/halo16 grid with replicated edges, as the reference's upscale does (aeisu/runtime.py:82-84),
+    and crops the 2H x 2W output back.  Each policy against its reference on the same FP16 frames: FP16
+    and FP32 against the FP32 model (1e-3 and 2e-5), Mixed and INT8 against their emulation (2/255),
+    and the fused kernels against the per-layer path bit for bit."""
+    from aeisu_amd import _lib as L
+    say(f"case: tiny/ragged frames {b}x3x{h}x{w}")
+    src16 = torch.stack([_frame(h, w, 60 + i) for i in range(b)]).half()
+    x = src16.cuda().contiguous()
+    fp32 = torch.stack([M.upscale(area_state, s.float(), 0) for s in src16])
+    fp32_model = R.load_model(WEIGHTS / "aeisu_area.pt", precision="fp32")
+    spyr = D.weights_from_spyr(spyr8f8.read_file(WEIGHTS / "aeisu_area_mixed_fp8.bin"))
+    int8 = D.weights_from_int8(torch.load(WEIGHTS / "aeisu_int8_fp16.pt", map_location="cpu", weights_only=True))
+    padded = pad_frame(src16.float())
+    # FP32 output against the FP32 model; FP16 output against the emulations, which round to FP16 too
+    f32, f16 = torch.float32, torch.float16
+    cases = ((fp16_model, fp32, f32, 1e-3), (fp32_model, fp32, f32, 2e-5),
+             (mixed_model, crop_output(D.forward(padded, spyr, "mixed", out_dtype=f16), h, w), f16, 2 / 255),
+             (int8_model, crop_output(D.forward(padded, int8, "int8", out_dtype=f16), h, w), f16, 2 / 255))
+    for model, ref, odt, tol in cases:
+        got = model.run(x, out_dtype=odt).float().cpu()
+        assert got.shape == (b, 3, 2 * h, 2 * w)
+        err = (got - ref).abs().max().item()
+        say(f"  {model.precision}: max|gpu - reference| = {err:.3g} (bound {tol:.3g})")
+        assert err <= tol
+        if model.precision != "fp32":                  # FP32 runs per-layer kernels only
+            assert torch.equal(model.run(x, out_dtype=odt, flags=L.FLAG_UNFUSED).float().cpu(), got)
+
+
 def test_mixed_matches_emulation(mixed_model, area_state):
     say("case: Mixed FP8/FP16 vs emulation (96x160)")
     w = D.weights_from_spyr(spyr8f8.read_file(WEIGHTS / "aeisu_area_mixed_fp8.bin"))
