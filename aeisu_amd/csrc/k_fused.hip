@@ -81,6 +81,7 @@ struct FusedLayout {
   static constexpr int Lds = OffRgb + 2 * SizeRgb;
   static_assert(Lds <= 160 * 1024, "fused kernel LDS exceeds the CU's 160 KB");
   static_assert(J * kFProducers == 2 * QH, "producers must split the tile's 16-pixel groups evenly");
+  static_assert(Consumers == 2 * QH, "the consumers produce the first tile, one group each");
 };
 
 struct FusedGeom {
@@ -142,10 +143,11 @@ __device__ __forceinline__ void patch_store(const PatchRegs<LY>& r, unsigned cha
 // patch operands one tap ahead; the tail fragments are loaded once per call and shared by the J
 // groups (loaded per group, and waited for right before use, they left the producer at a third of
 // its issue rate).
-template <typename LY, bool QC>
+// J = LY::J for the producer waves; the first tile of a launch is produced by the consumer waves
+// with J = 1 (one group each), so the consumers do not sit idle for a whole producer tile.
+template <typename LY, bool QC, int J = LY::J>
 __device__ __forceinline__ void produce(const unsigned char* smem, const unsigned char* lds_patch,
                                         unsigned char* lds_meta, int p, int lane) {
-  constexpr int J = LY::J;
   const int n = lane & 15, g = lane >> 4;
   const h8* wf = reinterpret_cast<const h8*>(smem + LY::OffW);
   const f4* bias = reinterpret_cast<const f4*>(smem + LY::OffBias);
@@ -374,8 +376,7 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
     }
   }
   lds_barrier();                                   // weights, biases and prologue loads visible
-  if (t0 < G.num_tiles) produce<LY, QC>(smem, smem + LY::OffPatch, smem + LY::OffMeta, wave, lane);
-  lds_barrier();                                   // coefficients of tile 0 visible
+  lds_barrier();                                   // coefficients of tile 0 (the consumers') visible
   const int iters = tile_iters(G.num_tiles);
   for (int it = 0; it < iters; ++it) {
     if (tile_of(it, G.num_tiles) >= G.num_tiles) break;   // block-uniform, as in consumer_main
@@ -421,6 +422,8 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
     rgb_store<Tin, Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb), ctid);
   }
   lds_barrier();                                   // prologue loads visible
+  // tile 0's coefficients: one 16-pixel group per consumer wave (2 QH groups, 2 QH consumers)
+  if (t0 < G.num_tiles) produce<LY, QC, 1>(smem, smem + LY::OffPatch, smem + LY::OffMeta, row, fresh(lane));
   lds_barrier();                                   // coefficients of tile 0 visible
   const int iters = tile_iters(G.num_tiles);
   for (int it = 0; it < iters; ++it) {
