@@ -348,12 +348,19 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       right[c] = left[c];
       permlane16_swap(left[c], right[c]);
     }
+    // both lane groups of a row pair hold the same values: groups 0 / 2 write channel 0 and groups
+    // 1 / 3 channel 1 in one store, then groups 0 / 2 channel 2
     const unsigned o0 = (unsigned)(((size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x) * sizeof(Tout));
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-      const unsigned off = inside && (g & 1) == 0 ? o0 + (unsigned)(c * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
-      if constexpr (std::is_same<Tout, float>::value) fstore_pair<Tout>(ob, off, left[c], right[c]);
-      else __builtin_amdgcn_raw_buffer_store_b32(pack_h2_clamp01(left[c], right[c]), ob, (int)off, 0, 0);
+    const int c01 = g & 1;
+    const unsigned off01 = inside ? o0 + (unsigned)(c01 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
+    const unsigned off2 = inside && c01 == 0 ? o0 + (unsigned)(2 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
+    if constexpr (std::is_same<Tout, float>::value) {
+      fstore_pair<Tout>(ob, off01, c01 ? left[1] : left[0], c01 ? right[1] : right[0]);
+      fstore_pair<Tout>(ob, off2, left[2], right[2]);
+    } else {
+      const unsigned p0 = pack_h2_clamp01(left[0], right[0]), p1 = pack_h2_clamp01(left[1], right[1]);
+      __builtin_amdgcn_raw_buffer_store_b32(c01 ? p1 : p0, ob, (int)off01, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(pack_h2_clamp01(left[2], right[2]), ob, (int)off2, 0, 0);
     }
   }
 }
