@@ -298,6 +298,7 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
   const __amdgpu_buffer_rsrc_t ob = frame_rsrc(out + (size_t)t.b * 3 * oplane, 3 * oplane * sizeof(Tout));
   const _Float16* mrow = reinterpret_cast<const _Float16*>(lds_meta) + (r >> 1) * kFQW * kFMPix;
   const int rho_y = (r & 1) << 1;
+  unsigned sv01[kFLW / 16], sv2[kFLW / 16], so01[kFLW / 16], so2[kFLW / 16];
 #pragma unroll
   for (int j = 0; j < kFLW / 16; ++j) {
     const int x = 2 * t.qx0 + 16 * j - G.px + n;
@@ -342,8 +343,7 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const bool inside = (unsigned)x < (unsigned)G.W;
     chk = fmaf(inside ? u[0] + u[1] + u[2] : 0.f, 0.0f, chk);
     // pair phases (TL, TR) and (BL, BR): after the swap lane groups 0 and 1 both hold
-    // (TL, TR), groups 2 and 3 both hold (BL, BR); groups 0 and 2 store each pair (the
-    // duplicates get an out-of-range offset: identical stores would still cost write traffic)
+    // (TL, TR), groups 2 and 3 both hold (BL, BR)
     // (FP16 output: the [0, 1] clamp rides on the packed convert, after the swap)
     float left[3], right[3];
 #pragma unroll
@@ -353,7 +353,11 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       permlane16_swap(left[c], right[c]);
     }
     // both lane groups of a row pair hold the same values: groups 0 / 2 write channel 0 and groups
-    // 1 / 3 channel 1 in one store, then groups 0 / 2 channel 2
+    // 1 / 3 channel 1 in one store, then groups 0 / 2 channel 2 (lanes with nothing to write get an
+    // out-of-range offset).  FP16 output: a chunk writes 64 bytes per row and channel, so the
+    // stores of chunks j - 1 and j are issued together and fill whole 128-byte lines; with the
+    // non-temporal hint, half lines written apart were each sent to memory as a partial line
+    // (write traffic 1.44x the output).
     const unsigned o0 = (unsigned)(((size_t)(2 * y + (g >> 1)) * (2 * G.W) + 2 * x) * sizeof(Tout));
     const int c01 = g & 1;
     const unsigned off01 = inside ? o0 + (unsigned)(c01 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
@@ -363,8 +367,16 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       fstore_pair<Tout>(ob, off2, left[2], right[2]);
     } else {
       const unsigned p0 = pack_h2_clamp01(left[0], right[0]), p1 = pack_h2_clamp01(left[1], right[1]);
-      __builtin_amdgcn_raw_buffer_store_b32(c01 ? p1 : p0, ob, (int)off01, 0, kStoreNonTemporal);
-      __builtin_amdgcn_raw_buffer_store_b32(pack_h2_clamp01(left[2], right[2]), ob, (int)off2, 0, kStoreNonTemporal);
+      sv01[j] = c01 ? p1 : p0;
+      sv2[j] = pack_h2_clamp01(left[2], right[2]);
+      so01[j] = off01;
+      so2[j] = off2;
+      if (j & 1) {
+#pragma unroll
+        for (int k = j - 1; k <= j; ++k) __builtin_amdgcn_raw_buffer_store_b32(sv01[k], ob, (int)so01[k], 0, kStoreNonTemporal);
+#pragma unroll
+        for (int k = j - 1; k <= j; ++k) __builtin_amdgcn_raw_buffer_store_b32(sv2[k], ob, (int)so2[k], 0, kStoreNonTemporal);
+      }
     }
   }
 }
