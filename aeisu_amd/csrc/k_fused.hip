@@ -21,7 +21,10 @@
 //    permuted on the host); FP16 coefficients go to an LDS buffer.  They also load the
 //    zero-padded work patch of tile i+2.
 //  * 2QH consumer waves run the head on tile i, one LR row each, reading coefficients and a
-//    clamped RGB tile from LDS, and load the RGB tile of tile i+1.
+//    clamped RGB tile from LDS, and load the RGB tile of tile i+1.  The first tile's
+//    coefficients are produced by the consumer waves (one 16-pixel group each).
+//  * Output stores carry the non-temporal hint, and with FP16 output two neighbouring chunks'
+//    stores are issued together so that each fills whole 128-byte lines.
 //  * Work patch, coefficients and RGB tile are double-buffered; one barrier per tile.
 //    MFMA-bound producers and VALU-bound consumers share each SIMD.
 //  * FP16 frames: QH = 6 (16 waves, 4 per SIMD, <= 128 VGPRs), the RGB tile stays FP16 in
