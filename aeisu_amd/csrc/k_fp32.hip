@@ -104,44 +104,54 @@ __global__ __launch_bounds__(kF32Threads) void f32_compress_kernel(const float* 
                     leaky01(acc[co + 2] + wc[8194 + co]), leaky01(acc[co + 3] + wc[8195 + co]));
 }
 
-// ---- grouped 3x3 (2 groups of 32 -> 32, zero padding) + LeakyReLU: one low pixel and group per
-// thread; blockIdx.y is the group, so the weight rows stay block-uniform (scalar loads) and a 1080p
-// layer runs four waves per SIMD instead of two
+// ---- grouped 3x3 (2 groups of 32 -> 32, zero padding) + LeakyReLU: a 16 x 16 tile of low pixels
+// per block (one pixel per thread) and one conv group (blockIdx.y), its 18 x 18 input halo staged in
+// LDS with coalesced loads (the group's 32 channels of a pixel, 36 floats apart: conflict-free
+// 16-byte reads), the weight rows block-uniform (scalar loads).  Read straight from memory, each
+// thread's 72 strided 16-byte loads made the layer 4x slower.
+constexpr int kF32GT = 16, kF32GH = kF32GT + 2, kF32GPix = 36;
 __global__ __launch_bounds__(kF32Threads) void f32_grouped_kernel(const float* __restrict__ in, const float* __restrict__ wl,
                                                                   float* __restrict__ out, int Hl, int Wl, int batch) {
-  const long idx = (long)blockIdx.x * kF32Threads + threadIdx.x;
-  if (idx >= (long)batch * Hl * Wl) return;
-  const int b = (int)(idx / ((long)Hl * Wl));
-  const int rem = (int)(idx - (long)b * Hl * Wl);
-  const int ly = rem / Wl, lx = rem - ly * Wl;
-  const int grp = blockIdx.y;
-  {
-    float acc[32];
+  __shared__ __attribute__((aligned(16))) float tile[kF32GH * kF32GH * kF32GPix];
+  const int tx_n = (Wl + kF32GT - 1) / kF32GT, ty_n = (Hl + kF32GT - 1) / kF32GT;
+  const int b = (int)blockIdx.x / (tx_n * ty_n), rem = (int)blockIdx.x - b * tx_n * ty_n;
+  const int y0 = (rem / tx_n) * kF32GT, x0 = (rem % tx_n) * kF32GT;
+  const int grp = blockIdx.y, tid = threadIdx.x;
+  // stage: 18 x 18 pixels x 8 float4 (the group's 32 channels), zero outside the low grid
+  for (int i = tid; i < kF32GH * kF32GH * 8; i += kF32Threads) {
+    const int pix = i >> 3, q = i & 7, py = pix / kF32GH, px = pix - py * kF32GH;
+    const int y = y0 + py - 1, x = x0 + px - 1;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (y >= 0 && y < Hl && x >= 0 && x < Wl)
+      v = *reinterpret_cast<const float4*>(in + (((size_t)b * Hl + y) * Wl + x) * 64 + 32 * grp + 4 * q);
+    *reinterpret_cast<float4*>(&tile[pix * kF32GPix + 4 * q]) = v;
+  }
+  __syncthreads();
+  const int ty = tid / kF32GT, tx = tid - ty * kF32GT;
+  float acc[32];
 #pragma unroll
-    for (int o = 0; o < 32; ++o) acc[o] = 0.f;
-    for (int tap = 0; tap < 9; ++tap) {
-      const int y = ly + tap / 3 - 1, x = lx + tap % 3 - 1;
-      const bool inside = y >= 0 && y < Hl && x >= 0 && x < Wl;
-      const float* src = in + (((size_t)b * Hl + (inside ? y : ly)) * Wl + (inside ? x : lx)) * 64 + 32 * grp;
-      for (int c0 = 0; c0 < 32; c0 += 4) {
-        float4 x4 = *reinterpret_cast<const float4*>(src + c0);
-        if (!inside) x4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+  for (int o = 0; o < 32; ++o) acc[o] = 0.f;
+  for (int tap = 0; tap < 9; ++tap) {
+    const float* src = &tile[((ty + tap / 3) * kF32GH + tx + tap % 3) * kF32GPix];
+    for (int c0 = 0; c0 < 32; c0 += 4) {
+      const float4 x4 = *reinterpret_cast<const float4*>(src + c0);
+      const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float* wr = wl + (tap * 32 + c0 + e) * 64 + 32 * grp;
+      for (int e = 0; e < 4; ++e) {
+        const float* wr = wl + (tap * 32 + c0 + e) * 64 + 32 * grp;
 #pragma unroll
-          for (int o = 0; o < 32; ++o) acc[o] = fmaf(xs[e], wr[o], acc[o]);
-        }
+        for (int o = 0; o < 32; ++o) acc[o] = fmaf(xs[e], wr[o], acc[o]);
       }
     }
-    float* dst = out + (size_t)idx * 64 + 32 * grp;
-#pragma unroll
-    for (int o = 0; o < 32; o += 4)
-      *reinterpret_cast<float4*>(dst + o) = make_float4(
-          leaky01(acc[o] + wl[18432 + 32 * grp + o]), leaky01(acc[o + 1] + wl[18433 + 32 * grp + o]),
-          leaky01(acc[o + 2] + wl[18434 + 32 * grp + o]), leaky01(acc[o + 3] + wl[18435 + 32 * grp + o]));
   }
+  const int ly = y0 + ty, lx = x0 + tx;
+  if (ly >= Hl || lx >= Wl) return;
+  float* dst = out + (((size_t)b * Hl + ly) * Wl + lx) * 64 + 32 * grp;
+#pragma unroll
+  for (int o = 0; o < 32; o += 4)
+    *reinterpret_cast<float4*>(dst + o) = make_float4(
+        leaky01(acc[o] + wl[18432 + 32 * grp + o]), leaky01(acc[o + 1] + wl[18433 + 32 * grp + o]),
+        leaky01(acc[o + 2] + wl[18434 + 32 * grp + o]), leaky01(acc[o + 3] + wl[18435 + 32 * grp + o]));
 }
 
 // ---- expand 1x1 (64 -> 128) + LeakyReLU, pixel_shuffle, + skip: one low pixel per thread ----------
@@ -342,7 +352,8 @@ hipError_t launch_f32_controller(int in_fp32, const void* src, const float* wimg
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (ev && (e = hipEventRecord(ev[2], stream)) != hipSuccess) return e;
   for (int l = 0; l < 4; ++l) {
-    hipLaunchKernelGGL(f32_grouped_kernel, dim3(f32_grid(lowpx), 2), dim3(kF32Threads), 0, stream, (const float*)dst[l],
+    const int gtiles = batch * ((Hl + kF32GT - 1) / kF32GT) * ((Wl + kF32GT - 1) / kF32GT);
+    hipLaunchKernelGGL(f32_grouped_kernel, dim3(gtiles, 2), dim3(kF32Threads), 0, stream, (const float*)dst[l],
                        wimg + kF32Grouped + l * kF32GroupedStride, dst[l + 1], Hl, Wl, batch);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
