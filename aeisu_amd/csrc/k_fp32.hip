@@ -198,27 +198,37 @@ __global__ __launch_bounds__(kF32Threads) void f32_expand_kernel(const float* __
   }
 }
 
-// ---- refine 3x3 (32 -> 64, zero padding) + LeakyReLU -> tail 1x1 (64 -> 64): one packed pixel ------
+// ---- refine 3x3 (32 -> 64) + LeakyReLU + tail 1x1 (64 -> 64): a 16 x 16 tile of packed pixels per
+// block (one pixel per thread), its 18 x 18 input halo (32 channels, 36 floats apart) staged in LDS
+// as in the grouped layers; the tail in two halves of 32 outputs (64 + 32 accumulators within 128
+// VGPRs: four waves per SIMD; all 64 + 64 took 129)
 __global__ __launch_bounds__(kF32Threads) void f32_refine_tail_kernel(const float* __restrict__ work,
                                                                       const float* __restrict__ wimg,
                                                                       float* __restrict__ meta, int Hq, int Wq, int batch) {
-  const long idx = (long)blockIdx.x * kF32Threads + threadIdx.x;
-  if (idx >= (long)batch * Hq * Wq) return;
-  const int b = (int)(idx / ((long)Hq * Wq));
-  const int rem = (int)(idx - (long)b * Hq * Wq);
-  const int qy = rem / Wq, qx = rem - qy * Wq;
+  __shared__ __attribute__((aligned(16))) float tile[kF32GH * kF32GH * kF32GPix];
+  const int tx_n = (Wq + kF32GT - 1) / kF32GT, ty_n = (Hq + kF32GT - 1) / kF32GT;
+  const int b = (int)blockIdx.x / (tx_n * ty_n), rem = (int)blockIdx.x - b * tx_n * ty_n;
+  const int y0 = (rem / tx_n) * kF32GT, x0 = (rem % tx_n) * kF32GT;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kF32GH * kF32GH * 8; i += kF32Threads) {
+    const int pix = i >> 3, q = i & 7, py = pix / kF32GH, px = pix - py * kF32GH;
+    const int y = y0 + py - 1, x = x0 + px - 1;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (y >= 0 && y < Hq && x >= 0 && x < Wq)
+      v = *reinterpret_cast<const float4*>(work + (((size_t)b * Hq + y) * Wq + x) * 32 + 4 * q);
+    *reinterpret_cast<float4*>(&tile[pix * kF32GPix + 4 * q]) = v;
+  }
+  __syncthreads();
+  const int ty = tid / kF32GT, tx = tid - ty * kF32GT;
   const float* wr = wimg + kF32Refine;
   const float* wt = wimg + kF32Tail;
   float r[64];
 #pragma unroll
   for (int co = 0; co < 64; ++co) r[co] = 0.f;
   for (int tap = 0; tap < 9; ++tap) {
-    const int y = qy + tap / 3 - 1, x = qx + tap % 3 - 1;
-    const bool inside = y >= 0 && y < Hq && x >= 0 && x < Wq;
-    const float* src = work + (((size_t)b * Hq + (inside ? y : qy)) * Wq + (inside ? x : qx)) * 32;
+    const float* src = &tile[((ty + tap / 3) * kF32GH + tx + tap % 3) * kF32GPix];
     for (int c0 = 0; c0 < 32; c0 += 4) {
-      float4 x4 = *reinterpret_cast<const float4*>(src + c0);
-      if (!inside) x4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 x4 = *reinterpret_cast<const float4*>(src + c0);
       const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -228,11 +238,11 @@ __global__ __launch_bounds__(kF32Threads) void f32_refine_tail_kernel(const floa
       }
     }
   }
+  const int qy = y0 + ty, qx = x0 + tx;
+  if (qy >= Hq || qx >= Wq) return;
 #pragma unroll
   for (int ci = 0; ci < 64; ++ci) r[ci] = leaky01(r[ci] + wr[18432 + ci]);
-  // the tail in two halves of 32 outputs: 64 + 32 accumulators stay within 128 VGPRs (four waves
-  // per SIMD; all 64 + 64 took 129)
-  float* out = meta + (size_t)idx * 64;
+  float* out = meta + (((size_t)b * Hq + qy) * Wq + qx) * 64;
   for (int h = 0; h < 64; h += 32) {
     float t[32];
 #pragma unroll
@@ -362,7 +372,8 @@ hipError_t launch_f32_controller(int in_fp32, const void* src, const float* wimg
                      (const float*)skip, wimg, work, Hl, Wl, batch);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (ev && (e = hipEventRecord(ev[4], stream)) != hipSuccess) return e;
-  hipLaunchKernelGGL(f32_refine_tail_kernel, dim3(f32_grid(packed)), dim3(kF32Threads), 0, stream, (const float*)work,
+  const int rtiles = batch * ((Hq + kF32GT - 1) / kF32GT) * ((Wq + kF32GT - 1) / kF32GT);
+  hipLaunchKernelGGL(f32_refine_tail_kernel, dim3(rtiles), dim3(kF32Threads), 0, stream, (const float*)work,
                      wimg, meta, Hq, Wq, batch);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   if (ev && (e = hipEventRecord(ev[5], stream)) != hipSuccess) return e;
