@@ -58,18 +58,21 @@ def build_abi_smoke() -> Path:
     return ABI_SMOKE
 
 
-PROBE_SRC = ROOT / "tests" / "mfma_fp8_probe.hip"
-PROBE = ROOT / "tests" / "mfma_fp8_probe"
+PROBES = {name: (ROOT / "tests" / f"{name}.hip", ROOT / "tests" / name)
+          for name in ("mfma_fp8_probe", "mfma_f16_probe")}
 
 
-def build_probe() -> Path:
-    """The GPU test program that measures the E4M3 MFMA's accumulation against the FP16 MFMA."""
-    cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
-           "-packed-fp32-ops", str(PROBE_SRC), "-o", str(PROBE)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"mfma_fp8_probe build failed:\n{res.stderr}")
-    return PROBE
+def build_probes() -> list:
+    """The GPU test programs that measure the MFMA instructions' accumulation against exact sums."""
+    out = []
+    for src, exe in PROBES.values():
+        cmd = [HIPCC, "-O2", "-std=c++17", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+               "-packed-fp32-ops", str(src), "-o", str(exe)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"{exe.name} build failed:\n{res.stderr}")
+        out.append(exe)
+    return out
 
 
 def build(jobs: int = 8) -> Path:
@@ -84,7 +87,7 @@ def build(jobs: int = 8) -> Path:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
     build_abi_smoke()
-    build_probe()
+    build_probes()
     return LIB
 
 

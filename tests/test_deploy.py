@@ -6,7 +6,8 @@ is pinned three ways, each chosen so that a plausible mistake fails:
 1. Rounding points, against a brute-force restatement in exact rational
    arithmetic (``fractions.Fraction`` rounded to nearest even at the stated
    precision) on inputs built to expose them: the FP32 MMA chain over K=32
-   chunks in the reference's order, the ``fmaf`` epilogues, the FP16 tail bias,
+   chunks in the reference's order, the K=16 chains of the FP16 layers
+   (project, refine, tail) with their FP32 bias add, slope and FP16 store, the ``fmaf`` epilogues, the FP16 tail bias,
    the FMA-contracted expand residual, saturating E4M3 and INT8 requantization.
 2. Every FP8 and INT8 layer against the FP32 checkpoint's layer applied to the
    same dequantized input: each output lies within the weight-quantization
@@ -23,7 +24,9 @@ is pinned three ways, each chosen so that a plausible mistake fails:
 ``test_planted_*`` plant the mistakes a restatement is likely to make in the
 oracle (``bias`` for ``bias_fp8``, an off-by-one activation-scale index, an
 unrounded tail bias, a split multiply-add in the expand residual, float64 sums
-instead of chunked FP32 accumulation, phase-major compress chunks) and assert
+instead of chunked FP32 accumulation, phase-major compress chunks, one rounding
+of an FP16 layer's whole sum, interleaved FP16 chunks, column-major refine
+taps) and assert
 that the corresponding check fails.
 """
 from __future__ import annotations
@@ -301,6 +304,134 @@ def test_planted_split_expand_residual_is_caught(monkeypatch, area_mixed):
                         + torch.as_tensor(c).float())
     with pytest.raises(AssertionError):
         check_expand_residual(area_mixed)
+
+
+def _fp16_inputs(rng, cin, h, wd, big_chunks):
+    """FP16 activations whose K=16 chunks alternate between large and tiny magnitudes (chunk c large
+    when c in big_chunks), random signs, a few FP16 subnormals and exact zeros."""
+    x = rng.standard_normal((1, cin, h, wd))
+    for c in range(cin // 16):
+        x[:, 16 * c:16 * c + 16] *= 2.0 ** (6 if c in big_chunks else -7)
+    x[rng.random(x.shape) < 0.03] = 0.0
+    sub = rng.random(x.shape) < 0.02
+    x[sub] = rng.integers(-1023, 1024, int(sub.sum())) * 2.0 ** -24
+    return x.astype(np.float16).astype(np.float32)
+
+
+def _brute_fp16_layer(x, w, pix, bias, slope, tail=False):
+    """FP32 accumulators and FP16 outputs of one pixel of an FP16 layer in exact rational arithmetic:
+    acc <- r32(acc + sum of a K=16 step) over the reference's steps (1x1: channels 16s..16s+15; 3x3:
+    taps row-major, each channels 0-15 then 16-31), then r32(acc + bias) (tail: + r16(bias)), the
+    slope for negative values, r16."""
+    _, y, xx = pix
+    cin, k = w.shape[1], w.shape[-1]
+    taps = [(r, s) for r in range(k) for s in range(k)]
+    accs, out = [], []
+    for o in range(w.shape[0]):
+        acc = Fr(0)
+        for r, s in taps:
+            yy, xs = y + r - k // 2, xx + s - k // 2
+            for c0 in range(0, cin, 16):
+                part = Fr(0)
+                if 0 <= yy < x.shape[2] and 0 <= xs < x.shape[3]:
+                    for c in range(c0, c0 + 16):
+                        part += f(x[0, c, yy, xs]) * f(w[o, c, r, s])
+                acc = r32(acc + part)
+        accs.append(acc)
+        if tail:
+            out.append(r16(r32(acc + r16(f(bias[o])))))
+            continue
+        v = r32(acc + f(bias[o]))
+        if v < 0:
+            v = r32(v * f(np.float32(slope)))
+        out.append(r16(v))
+    return accs, out
+
+
+def check_fp16_chain(w):
+    """D.fp16_chain (the FP32 accumulator) and D.project / D.refine / D.tail (the FP16 layer) equal the
+    rational restatement of the reference's K=16 MMA chains and epilogues (SrcPyrCudaRuntime.cu:2539-2547,
+    2568-2583; SrcPyrNativeFp16Refine.cuh:425-475, 494-538), on inputs whose chunks mix magnitudes so
+    that one rounding of the whole sum gives different accumulators somewhere."""
+    rng = np.random.default_rng(11)
+    single_differs = 0
+    for layer, cin, h, wd, big in (("project", 32, 3, 5, {0}), ("project", 32, 2, 4, {1}),
+                                   ("refine", 32, 3, 4, {0}), ("tail", 64, 2, 5, {0, 2})):
+        x = _fp16_inputs(rng, cin, h, wd, big)
+        xt = torch.from_numpy(x)
+        wt = np.asarray(w[layer + ".w"], np.float32)
+        fn = {"project": D.project, "refine": D.refine, "tail": D.tail}[layer]
+        got = fn(xt, w).numpy()
+        chain = D.fp16_chain(xt, w[layer + ".w"]).numpy()
+        once = F.conv2d(xt.double(), w[layer + ".w"].double(), padding=wt.shape[-1] // 2).float().numpy()
+        bias = np.asarray(w[layer + ".b"], np.float32)
+        for pix in [(0, yy, xx) for yy in range(h) for xx in range(wd)]:
+            accs, want = _brute_fp16_layer(x, wt, pix, bias, 0.1, tail=layer == "tail")
+            for o, (a, v) in enumerate(zip(accs, want)):
+                assert Fr(float(chain[0, o, pix[1], pix[2]])) == a, (layer, "acc", pix, o)
+                assert Fr(float(got[0, o, pix[1], pix[2]])) == v, (layer, pix, o)
+                single_differs += Fr(float(once[0, o, pix[1], pix[2]])) != a
+    # the inputs do exercise the chunking: one rounding of the exact total differs somewhere
+    assert single_differs > 0
+
+
+def test_fp16_chain_matches_rational_restatement(area_mixed):
+    check_fp16_chain(area_mixed)
+
+
+def test_fp16_chain_is_exact_on_wide_products():
+    """Steps whose products span more than float64's 53 bits (2^13 next to 2^-48) are still summed
+    exactly: 2^13 + 2^-11 and 2^13 - 2^-12 are float32 midpoints and the 2^-48 products decide them."""
+    x = np.zeros((1, 16, 1, 3), np.float32)
+    wt = np.zeros((2, 16, 1, 1), np.float32)
+    x[0, 0, 0, :] = 64.0
+    wt[:, 0] = 128.0                                      # 2^13
+    x[0, 1, 0, :] = [2.0 ** -24, -2.0 ** -24, 3 * 2.0 ** -24]
+    wt[:, 1] = 2.0 ** -24                                  # +-2^-48, 3 * 2^-48
+    x[0, 2, 0, :] = 2.0 ** -5
+    wt[:, 2, 0, 0] = [2.0 ** -6, -2.0 ** -7]               # 2^13 + 2^-11, 2^13 - 2^-12: midpoints
+    got = D.fp16_chain(torch.from_numpy(x), torch.from_numpy(wt)).numpy()
+    broken = 0
+    for p in range(3):
+        for o in range(2):
+            exact = sum((f(x[0, c, 0, p]) * f(wt[o, c, 0, 0]) for c in range(16)), Fr(0))
+            assert Fr(float(got[0, o, 0, p])) == r32(exact), (p, o)
+            broken += r32(exact) != r32(Fr(2) ** 13 + f(wt[o, 2, 0, 0]) * f(x[0, 2, 0, p]))
+    assert broken > 0                                       # the tiny products do break ties
+
+
+def test_planted_single_rounding_of_fp16_layers_is_caught(monkeypatch, area_mixed):
+    monkeypatch.setattr(D, "fp16_chain", lambda x, w: D._conv64(x, w))
+    with pytest.raises(AssertionError):
+        check_fp16_chain(area_mixed)
+
+
+def test_planted_interleaved_fp16_chunks_are_caught(monkeypatch, area_mixed):
+    real = D.fp16_steps
+
+    def interleaved(x, w):
+        if w.shape[-1] != 1:
+            return real(x, w)
+        n = x.shape[1] // 16
+        return [(x[:, c::n], w[:, c::n]) for c in range(n)]
+    monkeypatch.setattr(D, "fp16_steps", interleaved)
+    with pytest.raises(AssertionError):
+        check_fp16_chain(area_mixed)
+
+
+def test_planted_column_major_refine_taps_are_caught(monkeypatch, area_mixed):
+    real = D.fp16_steps
+
+    def column_major(x, w):
+        if w.shape[-1] != 3:
+            return real(x, w)
+        h, wd = x.shape[-2:]
+        xp = F.pad(x, (1, 1, 1, 1))
+        return [(xp[:, c:c + 16, r:r + h, s:s + wd], w[:, c:c + 16, r:r + 1, s:s + 1])
+                for s in range(3) for r in range(3) for c in (0, 16)]
+    monkeypatch.setattr(D, "fp16_steps", column_major)
+    with pytest.raises(AssertionError):
+        check_fp16_chain(area_mixed)
 
 
 def check_tail(w):
