@@ -1026,7 +1026,8 @@ static std::string startup_report(const Runtime& rt) {
     << g.py << " io=" << (g.in_fp32 ? "f32" : "f16") << '/' << (g.out_fp32 ? "f32" : "f16")
     << " body_tiles24_frames=" << g.body_split << " body_tiles24_cols=" << g.body_cols24
     << " body_exchange_tile=" << g.body_xc_tile << " weights_bytes=" << rt.w->bytes()
-    << " scratch_bytes=" << rt.scratch_bytes() << " shared_model_users=" << rt.model.use_count();
+    << " scratch_bytes=" << rt.scratch_bytes() << " static_scratch_bytes=" << kNoAllocScratchBytes
+    << " shared_model_users=" << rt.model.use_count();
   return r.str();
 }
 
@@ -1301,6 +1302,9 @@ int aeisu_controller_async(aeisu_runtime* h, const void* d_in, void* d_meta, voi
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
     if (!d_in || !d_meta) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null buffer");
+    if (rt.mode == aeisu::kModeFp32)
+      aeisu::fail(AEISU_ERR_STATE, "the FP32 policy has no FP16 coefficient stage; run the whole frame "
+                                   "(aeisu_upscale*) or configure an FP16 or quantized policy");
     aeisu::enqueue_controller(*rt.w, rt.g, rt.scratch(), d_in, d_meta, (hipStream_t)stream, nullptr);
   });
 }
@@ -1310,6 +1314,9 @@ int aeisu_head_async(aeisu_runtime* h, const void* d_in, const void* d_meta, voi
     Runtime& rt = runtime_of(h);
     aeisu::require_configured(rt);
     if (!d_in || !d_meta || !d_out) aeisu::fail(AEISU_ERR_INVALID_ARGUMENT, "null buffer");
+    if (rt.mode == aeisu::kModeFp32)
+      aeisu::fail(AEISU_ERR_STATE, "the FP32 policy has no FP16 coefficient stage; run the whole frame "
+                                   "(aeisu_upscale*) or configure an FP16 or quantized policy");
     aeisu::enqueue_head(*rt.w, rt.g, rt.scratch(), d_in, d_meta, d_out, (hipStream_t)stream);
   });
 }

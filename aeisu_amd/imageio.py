@@ -47,10 +47,11 @@ def paired_images(source, target) -> List[Tuple[Path, Path]]:
         for p in list_images(root):
             key = p.relative_to(root).with_suffix("").as_posix()
             if key in out:
-                raise ValueError(f"Ambiguous relative image stem: {key}")
+                raise ValueError(f"{root} holds two images with the relative stem {key!r}")
             out[key] = p
         return out
     a, b = index(Path(source)), index(Path(target))
     if not a or a.keys() != b.keys():
-        raise ValueError(f"Pair folders must have identical relative stems; inputs={len(a)}, targets={len(b)}")
+        raise ValueError(f"input and target folders differ in their relative stems "
+                         f"({len(a)} inputs, {len(b)} targets, {len(a.keys() ^ b.keys())} unmatched)")
     return [(a[k], b[k]) for k in sorted(a)]

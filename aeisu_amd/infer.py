@@ -6,7 +6,9 @@ Contract of the reference's CLI (infer.py:9-26): the same flags (``--tile`` is t
 size, a multiple of 32, 0 for the whole frame), 8-bit PNG outputs written with round-half-up,
 and no existing file is ever replaced.  Here the whole job is planned first: every source is
 paired with its destination and every destination is checked before the first image is
-decoded, so a conflict leaves the output tree untouched.  ``--precision`` picks the
+decoded, so a conflict leaves the output tree untouched; two sources that map to one PNG
+(x.jpg and x.png in one folder) are a conflict too, and each PNG is checked again just before
+it is written.  ``--precision`` picks the
 arithmetic policy of the loaded artifact (default: the file's natural one).  All arithmetic
 runs in the HIP runtime; there is no CPU path.
 """
@@ -20,7 +22,7 @@ from typing import List, Sequence
 from .imageio import list_images, read_rgb, save_rgb
 from .runtime import load_model, upscale
 
-PRECISIONS = ("fp16", "mixed", "mixed-fp8mma", "int8")
+PRECISIONS = ("fp16", "mixed", "mixed-fp8mma", "int8", "fp32")
 
 
 @dataclass(frozen=True)
@@ -38,7 +40,13 @@ def plan(source: Path, output: Path) -> List[Job]:
         jobs = [Job(p, output / p.relative_to(source).with_suffix(".png")) for p in list_images(source)]
     if not jobs:
         raise ValueError("No input images found")
-    clashes = [j.destination for j in jobs if j.destination.exists() or j.destination.resolve() == j.source.resolve()]
+    seen = set()
+    clashes = []
+    for j in jobs:
+        dest = j.destination.resolve()
+        if j.destination.exists() or dest == j.source.resolve() or dest in seen:
+            clashes.append(j.destination)
+        seen.add(dest)
     if clashes:
         raise FileExistsError(f"Refusing to overwrite: {clashes[0]}" +
                               (f" (and {len(clashes) - 1} more)" if len(clashes) > 1 else ""))
@@ -61,7 +69,10 @@ def main(argv: Sequence[str] | None = None) -> None:
     jobs = plan(args.input, args.output)
     model = load_model(args.checkpoint, args.device, args.precision)
     for n, job in enumerate(jobs, 1):
-        save_rgb(job.destination, upscale(model, read_rgb(job.source), args.tile))
+        result = upscale(model, read_rgb(job.source), args.tile)
+        if job.destination.exists():
+            raise FileExistsError(f"Refusing to overwrite: {job.destination}")
+        save_rgb(job.destination, result)
         print(f"[{n}/{len(jobs)}] {job.source.name} -> {job.destination}", flush=True)
 
 

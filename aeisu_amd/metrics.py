@@ -35,11 +35,13 @@ def _gaussian_window(size: int = 11, sigma: float = 1.5, device=None) -> torch.T
 def distortion(prediction: torch.Tensor, target: torch.Tensor, crop: int = 2) -> Dict[str, float]:
     """{'y_mse', 'y_psnr', 'y_ssim'} of a CHW prediction against a same-size CHW target."""
     if prediction.shape != target.shape or prediction.ndim != 3:
-        raise ValueError("Prediction and target must be same-size CHW RGB")
+        raise ValueError(f"distortion() compares two CHW images of one shape, got {tuple(prediction.shape)} "
+                         f"and {tuple(target.shape)}")
     if not (torch.isfinite(prediction).all() and torch.isfinite(target).all()):
-        raise ValueError("Prediction and target must be finite")
+        raise ValueError("distortion() got a non-finite value")
     if crop < 0 or min(prediction.shape[-2:]) < 11 + 2 * crop:
-        raise ValueError("Images are too small for the border crop and 11x11 SSIM window")
+        raise ValueError(f"a {prediction.shape[-2]}x{prediction.shape[-1]} image leaves no 11x11 SSIM window after "
+                         f"a {crop}-pixel border crop")
     a = prediction.clamp(0, 1).double()
     b = target.double()
     if crop:

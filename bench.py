@@ -13,12 +13,15 @@ Protocol:
      frame on the current stream: two for the quantized policies, three for FP16), bracketed by torch.cuda.synchronize():
      value = K / elapsed (frames/s).  The same is measured for replays of the
      per-frame HIP graph and reported beside it (--graph makes that the value).
+  1b. K steps processed synchronously, each between two HIP events on the launch
+     stream (the reference's per-frame Process() timing): median and p95 per step.
   2. K more steps launched eagerly with HIP events recorded on the launch
      stream around every kernel: per-kernel average durations -> roofline.
   3. CPU baseline: the FP32 oracle restatement of the reference PyTorch path
      (oracle/model.py, tile=0) on a bounded sample of the same frames.
 
-Prints ONE JSON line.  ``--gpus N`` with N > 1 exits: this build runs on one GPU.
+Prints ONE JSON line.  ``--table`` measures configurations 0-4 in one run (GPU and
+CPU baseline each) and prints one line per configuration plus a markdown table.  ``--gpus N`` with N > 1 exits: this build runs on one GPU.
 """
 from __future__ import annotations
 
@@ -38,11 +41,17 @@ MFMA_PEAK = {"fp16": 2.5e15, "fp8": 5.0e15, "int8": 5.0e15, "fp32": 157.3e12}   
 CTRL_MAC_FP16 = 256 + 4608 + 1024        # project + refine + tail, per LR pixel (paper tex:352-359)
 CTRL_MAC_LOW = 512 + 4608 + 512          # compress + 4 bottlenecks + expand
 WORKLOADS = {
+    0: dict(precision="fp32", weights="aeisu_area.pt", name="aeisu_area fp32 256x256->512x512 b1"),
     1: dict(precision="fp16", weights="aeisu_area.pt", name="aeisu_area fp16 1080p->4K b1"),
     2: dict(precision="mixed", weights="aeisu_area_mixed_fp8.bin", name="aeisu_area mixed-fp8/fp16 1080p->4K b1"),
     3: dict(precision="int8", weights="aeisu_int8_fp16.pt", name="aeisu int8/fp16 540p->1080p b8"),
     4: dict(precision="mixed", weights="aeisu_div2k_l1_mixed_fp8.bin", name="aeisu_div2k_l1 mixed 1440p->5K b4"),
 }
+
+
+# the FP32 model whose reference PyTorch path the CPU baseline runs for each configuration (the INT8
+# artifact of config 3 is quantized from aeisu_area.pt)
+CPU_MODEL = {0: "aeisu_area.pt", 1: "aeisu_area.pt", 2: "aeisu_area.pt", 3: "aeisu_area.pt", 4: "aeisu_div2k_l1.pt"}
 
 
 KERNEL_KEYS = {"project_kernel": "project", "body_fused_kernel": "body", "fused_tail_head_kernel": "refine_tail_head",
@@ -85,7 +94,7 @@ def cpu_model() -> str:
     return platform.machine()
 
 
-def cpu_baseline(frames_cpu, budget_s: float, min_frames: int = 5):
+def cpu_baseline(frames_cpu, budget_s: float, min_frames: int = 5, weights: str = "aeisu_area.pt"):
     """FP32 oracle (the reference PyTorch path restated) on whole frames: one warm-up frame, then at
     least ``min_frames`` timed frames, more while the budget lasts (BASELINE protocol: 1 + >= 5)."""
     import torch
@@ -93,7 +102,7 @@ def cpu_baseline(frames_cpu, budget_s: float, min_frames: int = 5):
     usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     threads = min(usable, int(os.environ.get("OMP_NUM_THREADS", usable)))
     torch.set_num_threads(threads)
-    state = M.load_folded(ROOT / "weights" / "aeisu_area.pt")
+    state = M.load_folded(ROOT / "weights" / weights)
     M.upscale(state, frames_cpu[0].float(), 0)             # warm-up: one whole frame
     done, t0 = 0, time.perf_counter()
     while done < min_frames or time.perf_counter() - t0 < budget_s:
@@ -103,11 +112,22 @@ def cpu_baseline(frames_cpu, budget_s: float, min_frames: int = 5):
     return {"value": done / elapsed, "unit": "frames/s", "cores": threads, "kind": "port",
             "ms_per_frame": 1000 * elapsed / done, "cpu_model": cpu_model(), "threads": threads,
             "sample": f"1 warm-up + {done} timed whole {frames_cpu.shape[-2]}x{frames_cpu.shape[-1]} frames through "
-                      f"oracle/model.py FP32 upscale(tile=0) (torch CPU, {threads} threads on {usable} usable "
-                      f"cores, {cpu_model()})"}
+                      f"oracle/model.py FP32 upscale(tile=0) of {weights} (torch CPU, {threads} threads on {usable} "
+                      f"usable cores, {cpu_model()})"}
 
 
-def main():
+def median_p95(samples):
+    """Median and 95th percentile of per-frame times as the reference's runtime test computes them
+    (SrcPyrRuntimeTest.cpp:137-151 median, mean of the middle two for an even count; :240 p95 =
+    sorted[min(n - 1, ceil(0.95 n) - 1)])."""
+    import math
+    v = sorted(samples)
+    n = len(v)
+    med = v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+    return med, v[min(n - 1, math.ceil(0.95 * n) - 1)]
+
+
+def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -130,34 +150,35 @@ def main():
                          "clocks a sustained load reaches")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (reference point for HBM counters)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
-              "(frames shard across GPUs with no exchange, see DESIGN.md)", file=sys.stderr)
-        sys.exit(2)
+    ap.add_argument("--table", action="store_true",
+                    help="configurations 0-4 in one run, each on the GPU and on the CPU baseline (1 warm-up + "
+                         ">= 5 frames): one JSON line per configuration, then a markdown table on stderr")
+    return ap.parse_args()
 
+
+def measure(args, config: int, size=None, batch=None, precision=None, cpu_budget: float = 0.0):
+    """GPU (and optionally CPU-baseline) measurement of one configuration; returns the JSON record."""
     import torch
     from aeisu_amd import frames as FR
     from aeisu_amd import runtime as R
     from aeisu_amd import _lib as L
 
-    wl = dict(WORKLOADS[args.config])
-    spec = dict(FR.CONFIGS[args.config])
-    size = None
-    if args.size:
-        size = tuple(int(v) for v in args.size.lower().split("x"))
+    wl = dict(WORKLOADS[config])
+    spec = dict(FR.CONFIGS[config])
+    if size:
         spec["height"], spec["width"] = size
-    if args.batch:
-        spec["batch"] = args.batch
-    if args.precision:
-        wl["precision"] = args.precision
-    sweep = bool(args.size or args.batch or args.precision)
+    if batch:
+        spec["batch"] = batch
+    if precision:
+        wl["precision"] = precision
+    sweep = bool(size or batch or precision)
     B, H, W = spec["batch"], spec["height"], spec["width"]
     dev = torch.device("cuda", 0)
-    log(f"bench: config {args.config} ({wl['name']}), generating {args.pool} frame batches")
-    pool_cpu = [FR.config_frames(args.config, seed=1000 * i, batch=B, size=size) for i in range(args.pool)]
+    log(f"bench: config {config} ({wl['name']}), generating {args.pool} frame batches")
+    pool_cpu = [FR.config_frames(config, seed=1000 * i, batch=B, size=size) for i in range(args.pool)]
     pool = [p.to(dev).contiguous() for p in pool_cpu]
-    outs = [torch.empty(B, 3, 2 * H, 2 * W, dtype=torch.float16, device=dev) for _ in pool]
+    io_dtype = pool[0].dtype                                   # FP16 frames (FP32 for config 0)
+    outs = [torch.empty(B, 3, 2 * H, 2 * W, dtype=io_dtype, device=dev) for _ in pool]
     model = R.load_model(ROOT / "weights" / wl["weights"], precision=wl["precision"])
     stream = torch.cuda.current_stream()
 
@@ -196,8 +217,23 @@ def main():
     log(f"bench: {eager_launch_ms:.4f} ms/step eager, {graph_ms:.4f} ms/step graph replay "
         f"(value from {'graph' if graph else 'eager'})")
 
+    # --- 1b. per-frame synchronous timing, the reference's Process() protocol ------------------------
+    # SrcPyrRuntimeTest.cpp:195-240: every frame is processed synchronously and timed with device
+    # events around it; the median and the 95th percentile over the frames are reported.  Here: HIP
+    # events on the launch stream around each eager frame, the host waiting for each frame's end.
+    per_frame = []
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(args.steps):
+        ev0.record(stream)
+        step(i, graph)
+        ev1.record(stream)
+        ev1.synchronize()
+        per_frame.append(ev0.elapsed_time(ev1))
+    frame_med, frame_p95 = median_p95(per_frame)
+    log(f"bench: per-frame synchronous median {frame_med:.4f} ms, p95 {frame_p95:.4f} ms")
+
     # --- 2. per-kernel HIP events on the launch stream ---------------------------------------------
-    hd = model.handle(B, H, W, torch.float16, torch.float16, L.FLAG_STAGE_TIMING | run_flags)
+    hd = model.handle(B, H, W, io_dtype, io_dtype, L.FLAG_STAGE_TIMING | run_flags)
     for i in range(min(args.warmup, 5)):
         L.check(L.lib().aeisu_upscale_async(hd.ptr, pool[i % len(pool)].data_ptr(), outs[i % len(pool)].data_ptr(),
                                             stream.cuda_stream))
@@ -215,7 +251,7 @@ def main():
     Hp, Wp = geometry(H, W)
     lr_px = B * H * W
     packed_px = B * (Hp // 2) * (Wp // 2)
-    s_io = 2                                                  # FP16 frames in and out
+    s_io = pool[0].element_size()                             # frame bytes per value in and out
     head_bytes = lr_px * (3 * s_io + 16 * 2 + 12 * s_io)      # RGB in + FP16 coefficients + 2x RGB out
     refine_bytes = packed_px * (32 * 2 + 64 * 2)              # FP16 refine input + FP16 coefficient output
     refine_flops = 2.0 * packed_px * (32 * 64 * 9 + 64 * 64)
@@ -228,7 +264,7 @@ def main():
     ctrl_flops16 = 2.0 * lr_px * CTRL_MAC_FP16
     ctrl_flops_low = 2.0 * lr_px * CTRL_MAC_LOW
     fused = not args.unfused and wl["precision"] != "fp32"   # fused body and fused refine+tail+head kernels
-    traffic = {} if sweep else measured_traffic(args.config)   # the profiles cover configs 1-4 as defined
+    traffic = {} if sweep else measured_traffic(config)       # the profiles cover configs 1-4 as defined
     kernels = {}
     proj_bytes = lr_px * 3 * s_io + packed_px * 32 * 2        # RGB in + FP16 skip out
     proj_flops = 2.0 * packed_px * 32 * 32                    # project 1x1, FP16 MFMA
@@ -304,9 +340,9 @@ def main():
         log(f"bench: copy calibration {args.copy_calibration} MiB x3 done")
 
     cpu = None
-    if args.cpu_budget > 0:
+    if cpu_budget > 0:
         log("bench: CPU baseline")
-        cpu = cpu_baseline(torch.cat(pool_cpu)[:2], args.cpu_budget)
+        cpu = cpu_baseline(torch.cat(pool_cpu)[:2], cpu_budget, weights=CPU_MODEL[config])
 
     # the body's launch shape as configured (tile sides, halo exchange) from the startup report
     report = dict(kv.split("=", 1) for kv in hd.report().split() if "=" in kv)
@@ -314,21 +350,24 @@ def main():
                    if k in report}
 
     fps = B * 1000.0 / ms_per_step
-    line = {
+    return {
         "metric": "frames/s (ms/frame) 1080p->4K batch-1 mixed FP8/FP16; % MFMA / HBM roofline",
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5), "ms_per_frame": round(ms_per_step / B, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": {"fp16": "fp16", "mixed": "fp8-e4m3/fp16", "mixed-fp8mma": "fp8-e4m3/fp16",
                   "int8": "int8/fp16", "fp32": "fp32"}[wl["precision"]],
-        "data": f"synthetic (aeisu_amd.frames config {args.config}, {args.pool} resident frames)",
-        "config": {"workload": wl["name"] + (" (sweep override)" if sweep else ""), "config_id": args.config,
+        "data": f"synthetic (aeisu_amd.frames config {config}, {args.pool} resident frames)",
+        "config": {"workload": wl["name"] + (" (sweep override)" if sweep else ""), "config_id": config,
                    "batch": B, "input": [3, H, W],
                    "output": [3, 2 * H, 2 * W], "precision": wl["precision"], "weights": wl["weights"],
+                   "io": str(io_dtype).replace("torch.", ""),
                    "timed": "graph replay" if graph else "eager launches",
                    "refine_tail_head": "two kernels" if args.unfused else "fused", "body_launch": body_launch},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "frame_ms": {"median": round(frame_med, 5), "p95": round(frame_p95, 5), "frames": len(per_frame),
+                     "protocol": "synchronous per-step HIP events on the launch stream (reference Process())"},
         "kernels": kernels,
         "stages_ms": {k: round(v, 5) for k, v in stages.items()},
         "eager_ms_per_step": round(eager_launch_ms, 5), "graph_ms_per_step": round(graph_ms, 5),
@@ -339,7 +378,41 @@ def main():
         "timing_frames": nframes,
         "clock_warmup": {"seconds": args.clock_warmup, "frames": n_warm},
     }
-    print(json.dumps(line), flush=True)
+
+
+def table_row(rec) -> str:
+    """One row of the GPU/CPU comparison table (ms per frame, frames/s, cores, roofline fractions)."""
+    b = rec["config"]["batch"]
+    cpu = rec["cpu_baseline"] or {}
+    head = rec["kernels"].get("refine_tail_head") or rec["kernels"].get("head")
+    return (f"| {rec['config']['config_id']} | {rec['config']['workload']} | {cpu.get('ms_per_frame', 0):.1f} | "
+            f"{cpu.get('value', 0):.2f} | {cpu.get('cores', '')} | {rec['ms_per_frame']:.4f} | {rec['value']:.0f} | "
+            f"{rec['frame_ms']['median'] / b:.4f} / {rec['frame_ms']['p95'] / b:.4f} | "
+            f"{100 * rec['controller']['mfma_frac']:.1f} | {100 * head['frac']:.1f} |")
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
+              "(frames shard across GPUs with no exchange, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if args.table:
+        rows = []
+        for config in sorted(WORKLOADS):
+            rec = measure(args, config, cpu_budget=max(args.cpu_budget, 1e-3))
+            print(json.dumps(rec), flush=True)
+            rows.append(table_row(rec))
+        log("| config | workload | CPU ms/frame | CPU frames/s | cores | GPU ms/frame | GPU frames/s | "
+            "GPU per-frame median / p95 ms | controller % MFMA peak | head % HBM peak |")
+        log("|---|---|---|---|---|---|---|---|---|---|")
+        for r in rows:
+            log(r)
+        return
+    size = tuple(int(v) for v in args.size.lower().split("x")) if args.size else None
+    rec = measure(args, args.config, size=size, batch=args.batch, precision=args.precision,
+                  cpu_budget=args.cpu_budget)
+    print(json.dumps(rec), flush=True)
 
 
 if __name__ == "__main__":

@@ -141,16 +141,21 @@ int aeisu_upscale_graph(aeisu_runtime* rt, const void* d_in, void* d_out, void* 
  * path like aeisu_upscale_async for the geometry given here, without aeisu_configure and without
  * allocating: the work tensor (and the FP16 policy's skip tensor) live in a static device array of
  * 72 MiB per GPU, enough for one 1920x1080 frame in every policy (a frame that needs more is
- * rejected with AEISU_ERR_INVALID_ARGUMENT).  Runs the runtime's current policy on its uploaded
+ * rejected with AEISU_ERR_INVALID_ARGUMENT).  The array is part of the library's code object: every
+ * GPU the library is loaded on holds it for the life of the process, whether or not this entry point
+ * is called; it is not counted by aeisu_persistent_bytes (a per-runtime figure) and is reported as
+ * static_scratch_bytes in aeisu_startup_report.  Runs the runtime's current policy on its uploaded
  * weights.  Every call on one GPU shares that array: calls that overlap on a GPU race.  Non-finite
  * reconstructions are not reported on this path. */
 int aeisu_upscale_noalloc(aeisu_runtime* rt, int batch, int height, int width, int in_layout, int out_layout,
                           const void* d_in, void* d_out, void* stream);
 
-/* Controller only: d_in -> packed FP16 coefficients d_meta [B][Hp/2][Wp/2][64]. */
+/* Controller only: d_in -> packed FP16 coefficients d_meta [B][Hp/2][Wp/2][64].
+ * The FP32 policy has no FP16 coefficient stage: AEISU_ERR_STATE. */
 int aeisu_controller_async(aeisu_runtime* rt, const void* d_in, void* d_meta, void* stream);
 
-/* Reconstruction head only, on caller-supplied coefficients (same layout as above). */
+/* Reconstruction head only, on caller-supplied coefficients (same layout as above).
+ * Not available under the FP32 policy (AEISU_ERR_STATE). */
 int aeisu_head_async(aeisu_runtime* rt, const void* d_in, const void* d_meta, void* d_out, void* stream);
 
 /* Synchronise `stream`, read and clear the non-finite flag: AEISU_OK or AEISU_ERR_NONFINITE. */
@@ -171,7 +176,9 @@ int aeisu_stage_timings(aeisu_runtime* rt, float ms[AEISU_STAGE_COUNT], int* fra
 int aeisu_reset_timings(aeisu_runtime* rt);
 
 /* Device bytes held by the runtime: every uploaded weight buffer of its (shared) model plus its own
- * scratch.  Replaces PersistentDeviceBytes (SrcPyrCudaRuntime.h:79). */
+ * scratch.  Replaces PersistentDeviceBytes (SrcPyrCudaRuntime.h:79).  The library's static scratch
+ * of aeisu_upscale_noalloc (72 MiB per GPU, held by the process, not by a runtime) is not included;
+ * the startup report states it. */
 size_t aeisu_persistent_bytes(const aeisu_runtime* rt);
 
 /* One-line description of the configuration (artifact hash, GPU, policy, kernels, geometry, bytes),

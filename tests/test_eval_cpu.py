@@ -112,3 +112,43 @@ def test_infer_plan_checks_every_destination_first(tmp_path):
     (tmp_path / "empty").mkdir()
     with pytest.raises(ValueError, match="No input images found"):
         plan(tmp_path / "empty", tmp_path / "o2")
+
+
+def test_infer_plan_rejects_two_sources_with_one_destination(tmp_path):
+    """x.jpg and x.png in one folder both map to out/x.png: the plan refuses the job (the reference
+    raises on the second write, infer.py:21-23) instead of letting one output replace the other."""
+    import numpy as np
+    from PIL import Image
+    from aeisu_amd.infer import plan
+    src = tmp_path / "in"
+    src.mkdir()
+    for name in ("x.jpg", "x.png", "z.tif"):
+        Image.fromarray(np.zeros((8, 8, 3), np.uint8)).save(src / name)
+    with pytest.raises(FileExistsError, match="Refusing to overwrite"):
+        plan(src, tmp_path / "out")
+    assert not (tmp_path / "out").exists()
+
+
+def test_infer_cli_accepts_fp32_policy():
+    from aeisu_amd.infer import PRECISIONS, parse_args
+    assert "fp32" in PRECISIONS
+    args = parse_args(["--checkpoint", "m.pt", "--input", "a", "--output", "b", "--precision", "fp32"])
+    assert args.precision == "fp32"
+
+
+def test_score_log_writes_reference_csv_and_infinity(tmp_path):
+    """per_image.csv columns and the "Infinity" encoding of a non-finite mean (the reference's
+    evaluation format, evaluate.py:46-53)."""
+    import csv
+    import math
+    from aeisu_amd.evaluate import ScoreLog
+    log = ScoreLog(tmp_path / "per_image.csv")
+    log.add("a", {"y_mse": 0.0, "y_psnr": math.inf, "y_ssim": 1.0})
+    log.add("b/c", {"y_mse": 1e-4, "y_psnr": 40.0, "y_ssim": 0.98})
+    log.close()
+    with (tmp_path / "per_image.csv").open() as fh:
+        rows = list(csv.DictReader(fh))
+    assert list(rows[0]) == ["image", "y_mse", "y_psnr", "y_ssim"]
+    assert [r["image"] for r in rows] == ["a", "b/c"] and rows[0]["y_psnr"] == "inf"
+    means = log.means()
+    assert means["y_psnr"] == "Infinity" and means["y_mse"] == pytest.approx(5e-5) and means["y_ssim"] == pytest.approx(0.99)

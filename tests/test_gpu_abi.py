@@ -74,3 +74,23 @@ def test_upscaler_shares_weights_and_bounds_handles(gpu):
     assert total == weights + sum(b - weights for b in per_handle)
     model.close()
     fresh.close()
+
+
+def test_fp32_policy_refuses_the_coefficient_stages(gpu):
+    """The FP32 policy has no FP16 coefficient stage: aeisu_controller_async / aeisu_head_async return
+    AEISU_ERR_STATE with a message instead of launching the FP16 kernels on absent weights."""
+    from aeisu_amd import _lib as L
+    from aeisu_amd import runtime as R
+    say("case: FP32 policy, controller() and head() refused with AEISU_ERR_STATE")
+    model = R.load_model(WEIGHTS / "aeisu_area.pt", precision="fp32")
+    frames = torch.rand(1, 3, 40, 56, device=gpu)
+    for call in (lambda: model.controller(frames),
+                 lambda: model.head(frames, torch.zeros(1, 48, 48, 64, dtype=torch.float16, device=gpu))):
+        with pytest.raises(L.AeisuError) as info:
+            call()
+        assert info.value.code == L.AEISU_ERR_STATE and "FP32 policy" in str(info.value)
+    out = model.run(frames)                                 # the whole frame still runs
+    torch.cuda.synchronize()
+    assert out.shape == (1, 3, 80, 112) and bool(torch.isfinite(out).all())
+    # the allocation-free entry point's static array (per GPU, held by the process) is reported
+    assert f"static_scratch_bytes={72 << 20}" in model.report()
