@@ -140,6 +140,50 @@ __device__ __forceinline__ void patch_store(const PatchRegs<LY>& r, unsigned cha
   }
 }
 
+// With two patch rows per producer wave (FP16 frames: PH = 8) the chunks take a row-wise mapping:
+// producer wave w loads patch rows 2w and 2w+1, whose 2 x 34 pixels are two contiguous 2176-byte
+// segments of the work tensor, and lane l takes chunks c = l + 64k of the two rows (k = 0..4,
+// c < 272).  Every chunk's offset is the lane's 16 l plus a wave-uniform row start and a constant,
+// and every LDS offset the lane's base plus 1280 k (consecutive patch rows are contiguous in LDS
+// too), so the fetch costs about four VALU instructions per chunk where the general mapping
+// (patch_fetch: one division, clamps and a 64-bit address per chunk) costs about thirty.  Chunks
+// outside the work tensor get an offset past the buffer's range, which the hardware reads as zero
+// (the zero padding of the refine convolution).
+constexpr int kOutOfRange = 0x7FFFFFF0;            // at or past num_records for every work tensor < 2 GiB
+template <typename LY>
+__device__ __forceinline__ void patch_fetch_rows(PatchRegs<LY>& r, const _Float16* __restrict__ work, FusedTile t,
+                                                 const FusedGeom& G, int wave, int lane) {
+  static_assert(LY::PH == 2 * kFProducers && LY::PW * 4 * 2 == 272 && LY::PatchPer == 5,
+                "two 34-pixel patch rows per producer wave, five chunks per lane");
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<_Float16*>(work) + (size_t)t.b * G.Hq * G.Wq * 32, 0, G.Hq * G.Wq * 64, kRawBufferWord3);
+  const int w = __builtin_amdgcn_readfirstlane(wave);
+  const int r0 = t.qy0 - 1 + 2 * w;                  // patch rows r0 and r0 + 1 (wave-uniform)
+  const bool ok0 = (unsigned)r0 < (unsigned)G.Hq, ok1 = (unsigned)(r0 + 1) < (unsigned)G.Hq;
+  const int s0 = r0 * G.Wq * 64, s1 = s0 + G.Wq * 64;
+  const int gx = t.qx0 - 1 + (lane >> 2);            // work column of chunk l
+  const int cb = (t.qx0 - 1) * 64 + lane * 16;       // chunk l's byte offset from its row's start
+  // offset of chunk l + 4 d of a row (d pixels to the right of chunk l), or out of range
+  auto at = [&](bool row_ok, int start, int d) {
+    return row_ok && (unsigned)(gx + d) < (unsigned)G.Wq ? start + cb + 64 * d : kOutOfRange;
+  };
+  const int o2 = lane < 8 ? at(ok0, s0, 32) : at(ok1, s1, -2);   // chunk 128 + l of row 0, or l - 8 of row 1
+  r.v[0] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, at(ok0, s0, 0), 0, 0));
+  r.v[1] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, at(ok0, s0, 16), 0, 0));
+  r.v[2] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, o2, 0, 0));
+  r.v[3] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, at(ok1, s1, 14), 0, 0));
+  // chunks 256..271 of the two rows (lanes 0..15); the other lanes' fifth load is out of range
+  r.v[4] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane < 16 ? at(ok1, s1, 30) : kOutOfRange, 0, 0));
+}
+template <typename LY>
+__device__ __forceinline__ void patch_store_rows(const PatchRegs<LY>& r, unsigned char* lds_patch, int wave, int lane) {
+  const int w = __builtin_amdgcn_readfirstlane(wave);
+  unsigned char* d = lds_patch + 2 * w * LY::PW * kFPix * 2 + ((lane >> 2) * kFPix + (lane & 3) * 8) * 2;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) *reinterpret_cast<u4*>(d + 1280 * k) = r.v[k];
+  if (lane < 16) *reinterpret_cast<u4*>(d + 5120) = r.v[4];
+}
+
 // refine + tail for 16-pixel groups p*J .. p*J+J-1 of the tile (group q: packed row q/2, half q%2).
 // One producer wave per SIMD runs this, so nothing hides its LDS latency: the operands are pipelined
 // by hand, each weight fragment loaded one (tap, T) step ahead of its three MFMAs and each tap's
@@ -236,18 +280,25 @@ struct RgbRegs {
 template <typename Tin, typename LY>
 __device__ __forceinline__ void rgb_fetch(RgbRegs<Tin, LY>& r, const Tin* __restrict__ src, FusedTile t,
                                           const FusedGeom& G, int ctid) {
-  const size_t plane = (size_t)G.H * G.W;
-  const Tin* s = src + (size_t)t.b * 3 * plane;
+  // one raw buffer per frame (3 planes < 2^31 bytes): 32-bit offsets, the plane as a scalar offset
+  const int plane = G.H * G.W * (int)sizeof(Tin);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<Tin*>(src) + (size_t)t.b * 3 * G.H * G.W, 0, 3 * plane, kRawBufferWord3);
   const int y0 = 2 * t.qy0 - G.py - 2, x0 = 2 * t.qx0 - G.px - 2;
 #pragma unroll
   for (int k = 0; k < LY::RgbPer; ++k) {
     const int q = min(ctid + LY::ConsumerThreads * k, LY::RPos - 1);
     const int ly = q / kFRW, lx = q - ly * kFRW;
-    const int sy = min(max(y0 + ly, 0), G.H - 1), sx = min(max(x0 + lx, 0), G.W - 1);
-    const size_t o = (size_t)sy * G.W + sx;
-    r.v[k][0] = s[o];
-    r.v[k][1] = s[plane + o];
-    r.v[k][2] = s[2 * plane + o];
+    const int sy = min(max(y0 + ly, 0), G.H - 1);
+    const int sx = min(max(x0 + lx, 0), G.W - 1);
+    const int o = (sy * G.W + sx) * (int)sizeof(Tin);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      if constexpr (sizeof(Tin) == 2)
+        r.v[k][c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, o, c * plane, 0));
+      else
+        r.v[k][c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, o, c * plane, 0));
+    }
   }
 }
 __device__ __forceinline__ void rgb_put(h4* d, _Float16 a, _Float16 b, _Float16 c) { *d = h4{a, b, c, (_Float16)0.0f}; }
@@ -412,11 +463,18 @@ __device__ __forceinline__ void producer_main(unsigned char* smem, const _Float1
     // they were spilled and their reloads waited for the patch prefetch
     const int ptid_it = fresh(ptid), lane_it = fresh(lane);
     PatchRegs<LY> pr;
-    if (tnn < G.num_tiles) patch_fetch<LY>(pr, work, fused_tile<LY::QH>(tnn, G), G, ptid_it);
+    if constexpr (LY::PH == 2 * kFProducers) {      // FP16 frames: the row-wise chunk mapping
+      if (tnn < G.num_tiles) patch_fetch_rows<LY>(pr, work, fused_tile<LY::QH>(tnn, G), G, wave, lane_it);
+    } else {
+      if (tnn < G.num_tiles) patch_fetch<LY>(pr, work, fused_tile<LY::QH>(tnn, G), G, ptid_it);
+    }
     if (tn < G.num_tiles)
       produce<LY, QC>(smem, smem + LY::OffPatch + nxt * LY::SizePatch, smem + LY::OffMeta + nxt * LY::SizeMeta,
                       wave, lane_it);
-    if (tnn < G.num_tiles) patch_store<LY>(pr, smem + LY::OffPatch + cur * LY::SizePatch, ptid_it);
+    if (tnn < G.num_tiles) {
+      if constexpr (LY::PH == 2 * kFProducers) patch_store_rows<LY>(pr, smem + LY::OffPatch + cur * LY::SizePatch, wave, lane_it);
+      else patch_store<LY>(pr, smem + LY::OffPatch + cur * LY::SizePatch, ptid_it);
+    }
     lds_barrier();
   }
 }
