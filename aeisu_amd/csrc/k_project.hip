@@ -38,31 +38,59 @@ constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
 template <bool PRECISE> constexpr int kPFeat = PRECISE ? 72 : 40;
 
 constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
-constexpr int kPStage = (3 * kPRgb + 255) / 256;         // staged RGB values per thread
+constexpr int kPRows = 3 * kPLH;                         // region rows of the three channels (54)
+constexpr int kPRowIters = (kPRows + 3) / 4;             // rows per wave (four waves)
+constexpr int kPExtra = kPRows * (kPLW - 64);            // values in columns 64..65 (108)
+static_assert(kPLW >= 64 && kPLW - 64 <= 2 && kPExtra <= 256, "one extra column value per thread");
 
 // The halo RGB of the next tile is held as raw frame values and converted when stored to
-// LDS (converting at load time would make the compiler wait for every load on the spot);
-// the loads are unconditional with the index clamped into the region.
+// LDS (converting at load time would make the compiler wait for every load on the spot).
+// Region rows are taken row-wise: wave w loads rows w, w + 4, ... of the 54 channel rows,
+// lane l column l, so a load is one buffer instruction with the lane's column offset (computed
+// once per tile) and a wave-uniform row offset; columns 64 and 65 of the 54 rows are one value
+// each for threads 0..107.  Coordinates are clamped to the source (replicate padding).
 template <typename Tin>
 struct ProjectStage {
-  Tin v[kPStage];
+  Tin v[kPRowIters];
+  Tin x;
 };
-// RGB of the halo region of a tile (padded LR origin (Y0, X0)), clamped to the source
-// (replicate padding), planar [c][r][col]; element i of the stage is region value
-// tid + 256 i.
 template <typename Tin>
 __device__ __forceinline__ void project_fetch(ProjectStage<Tin>& st, const Tin* __restrict__ src, int b, int Y0,
                                               int X0, int H, int W, int py, int px, int tid) {
-  const size_t plane = (size_t)H * W;
-  const Tin* s = src + (size_t)b * 3 * plane;
+  const int plane = H * W * (int)sizeof(Tin);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<Tin*>(src) + (size_t)b * 3 * H * W, 0, 3 * plane, kRawBufferWord3);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63;
+  const int vx = min(max(X0 + l - px, 0), W - 1) * (int)sizeof(Tin);
 #pragma unroll
-  for (int i = 0; i < kPStage; ++i) {
-    const int q = min(tid + 256 * i, 3 * kPRgb - 1);
-    const int c = q / kPRgb, rem = q - c * kPRgb;
-    const int r = rem / kPLW, col = rem - r * kPLW;
-    const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + col - px, 0), W - 1);
-    st.v[i] = s[c * plane + (size_t)sy * W + sx];
+  for (int i = 0; i < kPRowIters; ++i) {
+    const int R = min(w + 4 * i, kPRows - 1);            // wave-uniform
+    const int c = R / kPLH, r = R - c * kPLH;
+    const int sy = min(max(Y0 + r - py, 0), H - 1);
+    const int so = c * plane + sy * W * (int)sizeof(Tin);
+    if constexpr (sizeof(Tin) == 2) st.v[i] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, vx, so, 0));
+    else st.v[i] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, vx, so, 0));
   }
+  {
+    const int q = min(tid, kPExtra - 1);
+    const int R = q >> 1, col = 64 + (q & 1);
+    const int c = R / kPLH, r = R - c * kPLH;
+    const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + col - px, 0), W - 1);
+    const int o = (sy * W + sx) * (int)sizeof(Tin);
+    if constexpr (sizeof(Tin) == 2) st.x = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, o, c * plane, 0));
+    else st.x = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, o, c * plane, 0));
+  }
+}
+// Stage -> LDS (planar FP32 [c][r][col]); rows past the 54th were loaded clamped and are not stored.
+template <typename Tin>
+__device__ __forceinline__ void project_store(const ProjectStage<Tin>& st, float* rgb, int tid) {
+  const int w = tid >> 6, l = tid & 63;
+#pragma unroll
+  for (int i = 0; i < kPRowIters; ++i) {
+    const int R = w + 4 * i;
+    if (R < kPRows) rgb[R * kPLW + l] = (float)st.v[i];
+  }
+  if (tid < kPExtra) rgb[(tid >> 1) * kPLW + 64 + (tid & 1)] = (float)st.x;
 }
 
 template <typename Tin, bool PRECISE>
@@ -109,11 +137,7 @@ __global__ __launch_bounds__(256) void project_kernel(
     int b, qy0, qx0;
     origin(tidx, b, qy0, qx0);
     lds_barrier();                                    // previous tile's RGB reads done
-#pragma unroll
-    for (int i = 0; i < kPStage; ++i) {
-      const int q = tid + 256 * i;
-      if (q < 3 * kPRgb) (&rgb[0][0][0])[q] = (float)st.v[i];
-    }
+    project_store<Tin>(st, &rgb[0][0][0], tid);
     {
       const int tn = tile_of(it + 1, num_tiles);      // next tile's RGB in flight during this one
       if (tn < num_tiles) {
