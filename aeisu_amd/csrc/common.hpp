@@ -152,6 +152,23 @@ __device__ __forceinline__ unsigned pack_s8x4(int a, int b, int c, int d) {
   return (unsigned)(a & 255) | ((unsigned)(b & 255) << 8) | ((unsigned)(c & 255) << 16) |
          ((unsigned)(d & 255) << 24);
 }
+// quant_s8 of a product x = fl32(v * inv) in the low byte of the returned word: x is clamped to
+// [-127, 127] and 1.5 * 2^23 added.  The sum lies in [2^23, 2^24), where the unit in the last place
+// is 1, so the addition rounds x to the nearest integer, ties to even (rint), and leaves that integer
+// in the low mantissa bits in two's complement: the word is 0x4B400000 + q.  Clamping before
+// rounding gives the same code as after it, the bounds being integers.  Two instructions instead of
+// rint, clamp and a float -> int conversion.
+__device__ __forceinline__ unsigned s8_code_word(float x) {
+  return __builtin_bit_cast(unsigned, __builtin_amdgcn_fmed3f(x, -127.0f, 127.0f) + 12582912.0f);
+}
+// Low bytes of four words, a in byte 0 .. d in byte 3 (two v_perm_b32 and an or).
+__device__ __forceinline__ unsigned pack_low_bytes4(unsigned a, unsigned b, unsigned c, unsigned d) {
+  return __builtin_amdgcn_perm(b, a, 0x0c0c0400u) | __builtin_amdgcn_perm(d, c, 0x04000c0cu);
+}
+// Four INT8 codes (quant_s8 of the products a..d), packed as pack_s8x4 packs them.
+__device__ __forceinline__ unsigned quant_s8x4(float a, float b, float c, float d) {
+  return pack_low_bytes4(s8_code_word(a), s8_code_word(b), s8_code_word(c), s8_code_word(d));
+}
 
 __device__ __forceinline__ unsigned short f2h_bits(float v) {
   _Float16 h = (_Float16)v;
@@ -224,11 +241,9 @@ __device__ __forceinline__ float h2f_lo(unsigned w) {
 __device__ __forceinline__ float h2f_hi(unsigned w) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
 }
-// fl32(float(half) * s) as one v_fma_mix_f32: the FP16 operand widens exactly and adding -0
-// leaves every product (+-0 included) unchanged.
-// FP16 half of w times s in one v_fma_mix_f32 with a -0 addend, which equals the rounded product
-// bit for bit (x + -0 = x for every x, +0 included); the compiler turns fma(x, s, -0) into a
-// separate conversion and multiply.
+// fl32(float(half) * s) for the FP16 half of w as one v_fma_mix_f32 with a -0 addend: the FP16
+// operand widens exactly and x + -0 = x for every x (+0 included), so the result is the rounded
+// product bit for bit; the compiler turns fma(x, s, -0) into a separate conversion and multiply.
 __device__ __forceinline__ float h2f_lo_mul(unsigned w, float s) {
   float r;
   asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(s));
@@ -237,6 +252,26 @@ __device__ __forceinline__ float h2f_lo_mul(unsigned w, float s) {
 __device__ __forceinline__ float h2f_hi_mul(unsigned w, float s) {
   float r;
   asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(w), "v"(s));
+  return r;
+}
+// fmaf(a, b, float(h)) for the FP16 half h of w (HI: the high half) as one v_fma_mix_f32: the addend
+// widens exactly, so the single rounding is fmaf's.
+template <bool HI>
+__device__ __forceinline__ float fma_h16_addend(float a, float b, unsigned w) {
+  float r;
+  if constexpr (HI) asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(w));
+  else asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,0,1]" : "=v"(r) : "v"(a), "v"(b), "v"(w));
+  return r;
+}
+// fl32(float(x) + float(y)) for FP16 halves x of u and y of w (HX, HY: the high halves), as
+// x * 1 + y in one v_fma_mix_f32 (both widen exactly; one rounding).
+template <bool HX, bool HY>
+__device__ __forceinline__ float add_h16_h16(unsigned u, unsigned w) {
+  float r;
+  if constexpr (HX && HY) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(u), "v"(w));
+  else if constexpr (HX) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(u), "v"(w));
+  else if constexpr (HY) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(u), "v"(w));
+  else asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(u), "v"(w));
   return r;
 }
 

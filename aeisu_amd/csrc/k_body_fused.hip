@@ -172,27 +172,22 @@ __device__ __forceinline__ typename BodyFusedCfg<MODE>::Frag widen(RawOp<MODE> r
 
 // Epilogue of compress / bottleneck outputs, split in two so the per-value part can be spread
 // between MFMAs: act_value is the FP32 value before packing (the per-layer kernels' arithmetic:
-// FP16 leaky(acc + b); E4M3 leaky(fmaf(acc, s, b)) * (1/s_out); INT8 the same, rounded half to
-// even), pack_store writes 4 consecutive channels to LDS (0 outside the frame).
+// FP16 leaky(acc + b); E4M3 and INT8 leaky(fmaf(acc, s, b)) * (1/s_out)), pack_store writes 4
+// consecutive channels to LDS (0 outside the frame).
 template <int MODE>
 __device__ __forceinline__ float act_value(typename BodyFusedCfg<MODE>::Acc acc, int r, float bs, float sc,
                                            float inv_out) {
   if constexpr (MODE == 0) return leaky(acc[r] + bs, 0.1f);
   else if constexpr (MODE == 1 || MODE == 3) return leaky(fmaf(acc[r], sc, bs), 0.1f) * inv_out;
-  else return __builtin_rintf(leaky(fmaf((float)acc[r], sc, bs), 0.1f) * inv_out);
+  else return leaky(fmaf((float)acc[r], sc, bs), 0.1f) * inv_out;
 }
-// Byte codes of 4 consecutive channels (E4M3 saturating RNE, or INT8 clamped to +-127).
+// Byte codes of 4 consecutive channels (E4M3 saturating RNE, or INT8 rounded half to even and
+// clamped to +-127: quant_s8x4).
 template <int MODE>
 __device__ __forceinline__ unsigned pack_codes4(const float (&v)[4]) {
   static_assert(MODE != 0, "byte-activation policies");
-  if constexpr (MODE == 1 || MODE == 3) {
-    return pack_e4m3x4(v[0], v[1], v[2], v[3]);
-  } else {
-    int q[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) q[r] = (int)__builtin_amdgcn_fmed3f(v[r], -127.0f, 127.0f);
-    return pack_s8x4(q[0], q[1], q[2], q[3]);
-  }
+  if constexpr (MODE == 1 || MODE == 3) return pack_e4m3x4(v[0], v[1], v[2], v[3]);
+  else return quant_s8x4(v[0], v[1], v[2], v[3]);
 }
 template <int MODE>
 __device__ __forceinline__ void pack_store(unsigned char* dst, const float (&v)[4], bool inside) {
@@ -267,10 +262,10 @@ __device__ __forceinline__ void compress_mma(const u4 (&raw)[4], const FragSet<M
       const u4 r0 = raw[2 * k], r1 = raw[2 * k + 1];
 #pragma unroll
       for (int w = 0; w < 2; ++w) {
-        bop[w] = (int)pack_s8x4(quant_s8(h2f_lo(r0[2 * w]), inv_in), quant_s8(h2f_hi(r0[2 * w]), inv_in),
-                                quant_s8(h2f_lo(r0[2 * w + 1]), inv_in), quant_s8(h2f_hi(r0[2 * w + 1]), inv_in));
-        bop[2 + w] = (int)pack_s8x4(quant_s8(h2f_lo(r1[2 * w]), inv_in), quant_s8(h2f_hi(r1[2 * w]), inv_in),
-                                    quant_s8(h2f_lo(r1[2 * w + 1]), inv_in), quant_s8(h2f_hi(r1[2 * w + 1]), inv_in));
+        bop[w] = (int)quant_s8x4(h2f_lo_mul(r0[2 * w], inv_in), h2f_hi_mul(r0[2 * w], inv_in),
+                                 h2f_lo_mul(r0[2 * w + 1], inv_in), h2f_hi_mul(r0[2 * w + 1], inv_in));
+        bop[2 + w] = (int)quant_s8x4(h2f_lo_mul(r1[2 * w], inv_in), h2f_hi_mul(r1[2 * w], inv_in),
+                                     h2f_lo_mul(r1[2 * w + 1], inv_in), h2f_hi_mul(r1[2 * w + 1], inv_in));
       }
     } else if constexpr (MODE == 0) {
       bop = __builtin_bit_cast(h8, raw[k]);
@@ -526,10 +521,10 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
         const float inv_in = P.inv_in;
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-          bop[w] = (int)pack_s8x4(quant_s8(h2f_lo(r0[2 * w]), inv_in), quant_s8(h2f_hi(r0[2 * w]), inv_in),
-                                  quant_s8(h2f_lo(r0[2 * w + 1]), inv_in), quant_s8(h2f_hi(r0[2 * w + 1]), inv_in));
-          bop[2 + w] = (int)pack_s8x4(quant_s8(h2f_lo(r1[2 * w]), inv_in), quant_s8(h2f_hi(r1[2 * w]), inv_in),
-                                      quant_s8(h2f_lo(r1[2 * w + 1]), inv_in), quant_s8(h2f_hi(r1[2 * w + 1]), inv_in));
+          bop[w] = (int)quant_s8x4(h2f_lo_mul(r0[2 * w], inv_in), h2f_hi_mul(r0[2 * w], inv_in),
+                                   h2f_lo_mul(r0[2 * w + 1], inv_in), h2f_hi_mul(r0[2 * w + 1], inv_in));
+          bop[2 + w] = (int)quant_s8x4(h2f_lo_mul(r1[2 * w], inv_in), h2f_hi_mul(r1[2 * w], inv_in),
+                                       h2f_lo_mul(r1[2 * w + 1], inv_in), h2f_hi_mul(r1[2 * w + 1], inv_in));
         }
       } else {
         const u4 r = project_phase(slice, pf, bs0, bs1, k, lane);
@@ -729,26 +724,39 @@ __device__ __forceinline__ void expand_store(const BodyFusedArgs& P, int b, int 
   for (int T = 0; T < 8; ++T) {
     const f4 bs = *reinterpret_cast<const f4*>(cst + kCstExpand + 16 * T + 4 * g);
     const f4 sc = *reinterpret_cast<const f4*>(cst + kCstExpand + 128 + 16 * T + 4 * g);
-    const float s[4] = {h2f_lo(sk[T][0]), h2f_hi(sk[T][0]), h2f_lo(sk[T][1]), h2f_hi(sk[T][1])};
+    // the FP16 skip values enter as mixed-precision addends (v_fma_mix_f32, exact widening)
+    const unsigned s01 = sk[T][0], s23 = sk[T][1];
     float v[4];
     if constexpr (MODE == 0) {
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) v[r4] = (float)(_Float16)leaky(acc[T][r4] + bs[r4], 0.1f) + s[r4];
-    } else if constexpr (MODE == 1 || MODE == 3) {
-      const unsigned qq = pack_e4m3x4(leaky(fmaf(acc[T][0], sc[0], bs[0]), 0.1f) * inv_out,
-                                      leaky(fmaf(acc[T][1], sc[1], bs[1]), 0.1f) * inv_out,
-                                      leaky(fmaf(acc[T][2], sc[2], bs[2]), 0.1f) * inv_out,
-                                      leaky(fmaf(acc[T][3], sc[3], bs[3]), 0.1f) * inv_out);
-      v[0] = fmaf(e4m3_to_f32<0>(qq), s_out, s[0]);
-      v[1] = fmaf(e4m3_to_f32<1>(qq), s_out, s[1]);
-      v[2] = fmaf(e4m3_to_f32<2>(qq), s_out, s[2]);
-      v[3] = fmaf(e4m3_to_f32<3>(qq), s_out, s[3]);
+      // fl32(fp16(leaky(acc + b)) + skip): both FP16 operands of one v_fma_mix_f32
+      const unsigned e01 = pack_h2(leaky(acc[T][0] + bs[0], 0.1f), leaky(acc[T][1] + bs[1], 0.1f));
+      const unsigned e23 = pack_h2(leaky(acc[T][2] + bs[2], 0.1f), leaky(acc[T][3] + bs[3], 0.1f));
+      v[0] = add_h16_h16<false, false>(e01, s01);
+      v[1] = add_h16_h16<true, true>(e01, s01);
+      v[2] = add_h16_h16<false, false>(e23, s23);
+      v[3] = add_h16_h16<true, true>(e23, s23);
     } else {
+      float q[4];
+      if constexpr (MODE == 1 || MODE == 3) {
+        const unsigned qq = pack_e4m3x4(leaky(fmaf(acc[T][0], sc[0], bs[0]), 0.1f) * inv_out,
+                                        leaky(fmaf(acc[T][1], sc[1], bs[1]), 0.1f) * inv_out,
+                                        leaky(fmaf(acc[T][2], sc[2], bs[2]), 0.1f) * inv_out,
+                                        leaky(fmaf(acc[T][3], sc[3], bs[3]), 0.1f) * inv_out);
+        q[0] = e4m3_to_f32<0>(qq);
+        q[1] = e4m3_to_f32<1>(qq);
+        q[2] = e4m3_to_f32<2>(qq);
+        q[3] = e4m3_to_f32<3>(qq);
+      } else {
+        // the INT8 code as a float: clamp(rint(x), -127, 127) = float(quant_s8)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int qi = quant_s8(leaky(fmaf((float)acc[T][r4], sc[r4], bs[r4]), 0.1f), inv_out);
-        v[r4] = fmaf((float)qi, s_out, s[r4]);
+        for (int r4 = 0; r4 < 4; ++r4)
+          q[r4] = __builtin_amdgcn_fmed3f(__builtin_rintf(leaky(fmaf((float)acc[T][r4], sc[r4], bs[r4]), 0.1f) * inv_out),
+                                          -127.0f, 127.0f);
       }
+      v[0] = fma_h16_addend<false>(q[0], s_out, s01);
+      v[1] = fma_h16_addend<true>(q[1], s_out, s01);
+      v[2] = fma_h16_addend<false>(q[2], s_out, s23);
+      v[3] = fma_h16_addend<true>(q[3], s_out, s23);
     }
     wt[T][0] = pack_h2(v[0], v[1]);
     wt[T][1] = pack_h2(v[2], v[3]);
