@@ -47,20 +47,20 @@ __device__ __forceinline__ float d135_unfused(float u, float d, float m, float h
   return ((u - d) * a0 - m * a1) + h * a2;
 }
 
-// Features f[feature][phase] of a packed pixel from its 4x4 LR window w[channel][row][col]
-// (one halo pixel on each side of its 2x2 LR pixels).  The luma of the 16 window pixels feeds
-// the 3x3 stencils centred on each of the four LR pixels.
-__device__ __forceinline__ void window_features(const float (&w)[3][4][4], const Analysis& an, float (&f)[8][4]) {
-  float lw[4][4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      lw[a][b] = dot3_unfused(make_float3(w[0][a][b], w[1][a][b], w[2][a][b]), an.mix[0], an.mix[1], an.mix[2]);
+// Luma of one LR pixel (the window luma of the stencil features).
+__device__ __forceinline__ float luma(float r, float g, float b, const Analysis& an) {
+  return dot3_unfused(make_float3(r, g, b), an.mix[0], an.mix[1], an.mix[2]);
+}
+
+// Features f[feature][phase] of a packed pixel from the luma lw[row][col] of its 4x4 LR window
+// (one halo pixel on each side of its 2x2 LR pixels) and the RGB c[channel][i][j] of those 2x2
+// pixels: the basis projections of each pixel and the 3x3 luma stencils centred on it.
+__device__ __forceinline__ void luma_features(const float (&lw)[4][4], const float (&c)[3][2][2], const Analysis& an,
+                                              float (&f)[8][4]) {
 #pragma unroll
   for (int ph = 0; ph < 4; ++ph) {
     const int i = ph >> 1, j = ph & 1;
-    const float3 v = make_float3(w[0][i + 1][j + 1], w[1][i + 1][j + 1], w[2][i + 1][j + 1]);   // this phase's pixel
+    const float3 v = make_float3(c[0][i][j], c[1][i][j], c[2][i][j]);   // this phase's pixel
     f[0][ph] = dot3_unfused(v, an.basis[0], an.basis[1], an.basis[2]);
     f[1][ph] = dot3_unfused(v, an.basis[3], an.basis[4], an.basis[5]);
     f[2][ph] = dot3_unfused(v, an.basis[6], an.basis[7], an.basis[8]);
@@ -74,6 +74,22 @@ __device__ __forceinline__ void window_features(const float (&w)[3][4][4], const
     f[6][ph] = comb3(sub_rn(dr, ul), an.d45[0], vmid, an.d45[1], hmid, an.d45[2]);
     f[7][ph] = d135_unfused(ur, dl, vmid, hmid, an.d135[0], an.d135[1], an.d135[2]);
   }
+}
+
+// The same from the 4x4 LR window w[channel][row][col] itself.
+__device__ __forceinline__ void window_features(const float (&w)[3][4][4], const Analysis& an, float (&f)[8][4]) {
+  float lw[4][4], c[3][2][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) lw[a][b] = luma(w[0][a][b], w[1][a][b], w[2][a][b], an);
+#pragma unroll
+  for (int ch = 0; ch < 3; ++ch)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) c[ch][i][j] = w[ch][i + 1][j + 1];
+  luma_features(lw, c, an, f);
 }
 
 // The same from LDS: channel c of window pixel (a, b) is p[c * plane + a * rs + b].

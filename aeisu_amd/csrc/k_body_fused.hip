@@ -356,15 +356,20 @@ __device__ __forceinline__ void fb_compress(const BodyFusedArgs& P, BodyTileF t,
 // ---- frame input: RGB staging, analysis features and project per 16-pixel group -----------------
 // A group of a flattened region (side S >= 16, low-grid origin (oy, ox)) covers at most two row
 // segments: m pixels of region row r from column c, then 16 - m pixels of row r + 1 from column 0.
-// Its RGB stage holds, per channel, the 6 padded-LR rows 4 ly - 1 .. 4 ly + 4 of each segment's
-// low row ly, side by side: segment 1 in stage columns 0 .. 4m + 1, segment 2 after it.
-constexpr int kSW = 68, kSR = 6;                      // stage row width, rows per channel
-constexpr int kSPlane = kSR * kSW;                   // floats per channel
+// Its stage covers the 6 padded-LR rows 4 ly - 1 .. 4 ly + 4 of each segment's low row ly, side by
+// side: segment 1 in stage columns 0 .. 4m + 1, segment 2 after it (68 columns in all).  The stage
+// holds the luma of every stage pixel (kSR rows of kSW floats), computed once per LR pixel, and the
+// RGB of the four middle rows, the packed pixels' own (channel-major, rows of kRW floats, stage
+// column j at j + 1, so that each packed pixel's 2 x 2 RGB starts on an even float).
+constexpr int kSW = 68, kSR = 6;                      // stage row width, rows
+constexpr int kSPlane = kSR * kSW;                   // luma floats
+constexpr int kRW = kSW + 2, kRPlane = 4 * kRW;      // RGB row width, floats per RGB channel
 constexpr int kFRow = 40;                            // halves per feature row (32 + 8 pad)
-constexpr int kSlice = 64 * kFRow * 2;               // bytes of a wave's slice (features >= RGB)
+constexpr int kSlice = 64 * kFRow * 2;               // bytes of a wave's slice (features >= stage)
 static_assert(kSlice == kBodySliceBytes, "slice size");
-static_assert(3 * kSPlane * 4 <= kSlice, "RGB stage must fit the slice");
-constexpr int kStageLoads = (3 * kSPlane + 63) / 64; // staged values per lane (19 rows x 64 + rest)
+static_assert((kSPlane + 3 * kRPlane) * 4 <= kSlice, "stage must fit the slice");
+constexpr int kStageLoads = 3 * kSR + 3;             // per lane: column `lane` (6 rows x 3 channels)
+                                                     // and one pixel of columns 64..67 (lanes < 24)
 
 struct GroupGeom {
   int ly, lx1, lx2, m;                               // segment 1 row / first column, segment 2 first column
@@ -394,76 +399,99 @@ struct RgbStage<_Float16> {
   __device__ __forceinline__ void set(int e, _Float16 x) { v[e >> 1][e & 1] = x; }
   __device__ __forceinline__ float get(int e) const { return (float)v[e >> 1][e & 1]; }
 };
-// Values of stage column j (lanes take j = lane for the first 64 columns of every channel
-// row; columns 64..67 of the 18 channel rows are spread over the remaining loads).  Loads are
-// unconditional with clamped coordinates (replicate padding of aeisu/runtime.py:84), held raw.
+// Lane L takes stage column L (rows 0..5, value c * kSR + row) and, for L < 24, the pixel (row
+// L >> 2, column 64 + (L & 3)) (values 3 kSR + c).  Loads are unconditional with clamped
+// coordinates (replicate padding of aeisu/runtime.py:84), held raw, through one raw buffer per
+// frame (three planes < 2^31 bytes): 32-bit offsets, the plane as a scalar offset.
 __device__ __forceinline__ int stage_src_x(const GroupGeom& gg, int j, int px, int W) {
   const int seg2 = j >= 4 * gg.m + 2;
   const int X = seg2 ? 4 * gg.lx2 - 1 + (j - 4 * gg.m - 2) : 4 * gg.lx1 - 1 + j;
   return min(max(X - px, 0), W - 1);
 }
 template <typename Tin>
+__device__ __forceinline__ Tin stage_load(__amdgpu_buffer_rsrc_t rs, int off, int soff) {
+  if constexpr (sizeof(Tin) == 2) return __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, off, soff, 0));
+  else return __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, off, soff, 0));
+}
+template <typename Tin>
 __device__ __forceinline__ void stage_fetch(RgbStage<Tin>& st, const Tin* __restrict__ frame, const GroupGeom& gg,
                                             const BodyFusedArgs& P, int lane) {
-  const size_t plane = (size_t)P.H * P.W;
+  const int plane = P.H * P.W * (int)sizeof(Tin), rowb = P.W * (int)sizeof(Tin);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<Tin*>(frame), 0, 3 * plane, kRawBufferWord3);
   {
     const int j = lane;
-    const int sx = stage_src_x(gg, j, P.px, P.W);
+    const int sx = stage_src_x(gg, j, P.px, P.W) * (int)sizeof(Tin);
     const int Y0 = 4 * gg.ly - 1 + (j >= 4 * gg.m + 2 ? 4 : 0) - P.py;
 #pragma unroll
     for (int row = 0; row < kSR; ++row) {
-      const size_t o = (size_t)min(max(Y0 + row, 0), P.H - 1) * P.W + sx;
+      const int o = min(max(Y0 + row, 0), P.H - 1) * rowb + sx;
 #pragma unroll
-      for (int c = 0; c < 3; ++c) st.set(c * kSR + row, frame[c * plane + o]);
+      for (int c = 0; c < 3; ++c) st.set(c * kSR + row, stage_load<Tin>(rs, o, c * plane));
     }
   }
-#pragma unroll
-  for (int e = 3 * kSR; e < kStageLoads; ++e) {
-    const int v = min(lane + 64 * (e - 3 * kSR), 3 * kSR * (kSW - 64) - 1);
-    const int rc = v >> 2, j = 64 + (v & 3);
-    const int c = rc / kSR, row = rc - c * kSR;
-    const int sx = stage_src_x(gg, j, P.px, P.W);
+  {
+    const int v = min(lane, 4 * kSR - 1), row = v >> 2, j = 64 + (v & 3);
+    const int sx = stage_src_x(gg, j, P.px, P.W) * (int)sizeof(Tin);
     const int Y = 4 * gg.ly - 1 + (j >= 4 * gg.m + 2 ? 4 : 0) + row - P.py;
-    st.set(e, frame[c * plane + (size_t)min(max(Y, 0), P.H - 1) * P.W + sx]);
+    const int o = min(max(Y, 0), P.H - 1) * rowb + sx;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) st.set(3 * kSR + c, stage_load<Tin>(rs, o, c * plane));
   }
 }
 template <typename Tin>
-__device__ __forceinline__ void stage_store(const RgbStage<Tin>& st, float* stg, int lane) {
+__device__ __forceinline__ void stage_store(const RgbStage<Tin>& st, float* stg, const Analysis& an, int lane) {
+  float* rgb = stg + kSPlane;
 #pragma unroll
-  for (int c = 0; c < 3; ++c)
-#pragma unroll
-    for (int row = 0; row < kSR; ++row) stg[c * kSPlane + row * kSW + lane] = st.get(c * kSR + row);
-#pragma unroll
-  for (int e = 3 * kSR; e < kStageLoads; ++e) {
-    const int v = lane + 64 * (e - 3 * kSR);
-    if (v < 3 * kSR * (kSW - 64)) {
-      const int rc = v >> 2, j = 64 + (v & 3);
-      stg[(rc / kSR) * kSPlane + (rc % kSR) * kSW + j] = st.get(e);
+  for (int row = 0; row < kSR; ++row) {
+    const float r = st.get(row), g = st.get(kSR + row), b = st.get(2 * kSR + row);
+    stg[row * kSW + lane] = luma(r, g, b, an);
+    if (row >= 1 && row <= 4) {
+      float* d = rgb + (row - 1) * kRW + lane + 1;
+      d[0] = r;
+      d[kRPlane] = g;
+      d[2 * kRPlane] = b;
+    }
+  }
+  if (lane < 4 * kSR) {
+    const int row = lane >> 2, j = 64 + (lane & 3);
+    const float r = st.get(3 * kSR), g = st.get(3 * kSR + 1), b = st.get(3 * kSR + 2);
+    stg[row * kSW + j] = luma(r, g, b, an);
+    if (row >= 1 && row <= 4) {
+      float* d = rgb + (row - 1) * kRW + j + 1;
+      d[0] = r;
+      d[kRPlane] = g;
+      d[2 * kRPlane] = b;
     }
   }
 }
 
-// Features of the lane's packed pixel (phase g of low pixel n of the group) from the staged
-// RGB into feature row `lane` of the slice.  The rows overwrite the stage: every lane's stage
-// reads were issued before (a wave's LDS operations execute in order).
+// Features of the lane's packed pixel (phase g of low pixel n of the group) from the stage into
+// feature row `lane` of the slice.  The rows overwrite the stage: every lane's stage reads were
+// issued before (a wave's LDS operations execute in order).
 __device__ __forceinline__ void features_to_slice(unsigned char* slice, int m, const Analysis& an, int lane) {
   const int n = lane & 15, g = lane >> 4;
-  // window origin: an even stage column, so each window row is two aligned float2 reads; all
-  // 24 reads are issued before the arithmetic
-  const int col = 4 * n + 2 * (g & 1) + (n >= m ? 2 : 0);
-  const float* p = reinterpret_cast<const float*>(slice) + 2 * (g >> 1) * kSW + col;
-  float w[3][4][4];
+  // window origin: an even stage column, so each luma row is two aligned float2 reads and each
+  // RGB row of the 2 x 2 pixels one; all 14 reads are issued before the arithmetic
+  const int col = 4 * n + 2 * (g & 1) + (n >= m ? 2 : 0), r0 = 2 * (g >> 1);
+  const float* lp = reinterpret_cast<const float*>(slice) + r0 * kSW + col;
+  const float* cp = reinterpret_cast<const float*>(slice) + kSPlane + r0 * kRW + col + 2;
+  float lw[4][4], c[3][2][2];
 #pragma unroll
-  for (int c = 0; c < 3; ++c)
+  for (int a = 0; a < 4; ++a) {
+    const float2 lo = *reinterpret_cast<const float2*>(lp + a * kSW);
+    const float2 hi = *reinterpret_cast<const float2*>(lp + a * kSW + 2);
+    lw[a][0] = lo.x; lw[a][1] = lo.y; lw[a][2] = hi.x; lw[a][3] = hi.y;
+  }
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const float2 lo = *reinterpret_cast<const float2*>(p + c * kSPlane + a * kSW);
-      const float2 hi = *reinterpret_cast<const float2*>(p + c * kSPlane + a * kSW + 2);
-      w[c][a][0] = lo.x; w[c][a][1] = lo.y; w[c][a][2] = hi.x; w[c][a][3] = hi.y;
+  for (int ch = 0; ch < 3; ++ch)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float2 v = *reinterpret_cast<const float2*>(cp + ch * kRPlane + i * kRW);
+      c[ch][i][0] = v.x; c[ch][i][1] = v.y;
     }
   __builtin_amdgcn_sched_barrier(0);
   float f[8][4];
-  window_features(w, an, f);
+  luma_features(lw, c, an, f);
   h8 hi[4], lo[4];
   feature_slices<false>(f, hi, lo);
   _Float16* feat = reinterpret_cast<_Float16*>(slice);
@@ -503,7 +531,7 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
   const int g = lane >> 4;
   const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
   for (int pg = wave, next; pg < G; pg = next) {
-    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), lane);
+    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), an, lane);
     features_to_slice(slice, group_geom(t.y0 - O, t.x0 - O, S, pg).m, an, lane);
     next = claim_group(counter, lane);
     if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0 - O, t.x0 - O, S, next), P, lane);
@@ -820,7 +848,7 @@ __device__ __forceinline__ void fb_expand_rgb(const BodyFusedArgs& P, BodyTileF 
   const int n = lane & 15, g = lane >> 4;
   const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
   for (int pg = wave, next; pg < G; pg = next) {
-    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), lane);
+    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), an, lane);
     features_to_slice(slice, group_geom(t.y0, t.x0, S, pg).m, an, lane);
     next = claim_group(counter, lane);
     if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, S, next), P, lane);
