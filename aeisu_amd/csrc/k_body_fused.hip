@@ -517,8 +517,23 @@ __device__ __forceinline__ u4 project_phase(const unsigned char* slice, const h8
   return sk;
 }
 
+// Skip hand-over between the frame-input compress and expand of a tile.  Compress computes the
+// skip values (the project output) of every pixel of its region, and the tile's expand needs them
+// again for the core's residual.  Compress stores them for the core pixels into the block's own
+// part of the work tensor -- the 64 bytes of each packed pixel, in the project accumulator layout
+// (lane group g's 16 bytes at byte 16g: channels 4g..4g+3, 16+4g..16+4g+3) -- and expand reads
+// them back before it overwrites the same bytes with its output (each pixel's reads precede its
+// writes through the data dependence).  The cores of a launch's tiles are disjoint, so a pixel is
+// written and read by one block only; its stores are complete (vmcnt(0)) before the barrier that
+// ends compress, and no CU has the lines cached before (none reads them earlier in the kernel).
+__device__ __forceinline__ _Float16* skip_slot(const BodyFusedArgs& P, int b, int ly, int lx, int ph, int g) {
+  const int Hq = 2 * P.Hl, Wq = 2 * P.Wl;
+  return P.work + ((((size_t)b * Hq + 2 * ly + (ph >> 1)) * Wq + 2 * lx + (ph & 1)) * 32 + 8 * g);
+}
+
 // Frame-input compress (quantized policies).  Per group: stage -> features -> next group's RGB
-// loads issued -> per compress K-chunk, the project MFMAs of its phases and the compress MFMAs.
+// loads issued -> per compress K-chunk, the project MFMAs of its phases (their FP16 outputs of
+// core pixels kept for expand, skip_slot) and the compress MFMAs.
 // CORE: the T x T core only (compress exchange), else the whole region R0.
 template <int MODE, typename Tin, int TT = BodyFusedCfg<MODE>::T, bool CORE = false>
 __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTileF t, unsigned char* dst,
@@ -537,6 +552,10 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
     if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0 - O, t.x0 - O, S, next), P, lane);
     const f4 bs0 = *reinterpret_cast<const f4*>(cst + kCstProject + 4 * g);
     const f4 bs1 = *reinterpret_cast<const f4*>(cst + kCstProject + 16 + 4 * g);
+    // the lane's low pixel; is it a core pixel of this tile inside the low grid?
+    const int q = pg * 16 + (lane & 15), r = q / S, c = q - r * S;
+    const int ly = t.y0 - O + r, lx = t.x0 - O + c;
+    const bool keep = (q < N) & (r >= O) & (r < O + C::T) & (c >= O) & (c < O + C::T) & (ly < P.Hl) & (lx < P.Wl);
     typename C::Acc acc[4];
 #pragma unroll
     for (int T = 0; T < 4; ++T) acc[T] = typename C::Acc{};
@@ -546,6 +565,10 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
       if constexpr (MODE == 2) {
         const u4 r0 = project_phase(slice, pf, bs0, bs1, 2 * k, lane);
         const u4 r1 = project_phase(slice, pf, bs0, bs1, 2 * k + 1, lane);
+        if (keep) {
+          *reinterpret_cast<u4*>(skip_slot(P, t.b, ly, lx, 2 * k, g)) = r0;
+          *reinterpret_cast<u4*>(skip_slot(P, t.b, ly, lx, 2 * k + 1, g)) = r1;
+        }
         const float inv_in = P.inv_in;
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
@@ -556,6 +579,7 @@ __device__ __forceinline__ void fb_compress_rgb(const BodyFusedArgs& P, BodyTile
         }
       } else {
         const u4 r = project_phase(slice, pf, bs0, bs1, k, lane);
+        if (keep) *reinterpret_cast<u4*>(skip_slot(P, t.b, ly, lx, k, g)) = r;
         const float inv_in = P.inv_in;
         const unsigned lo = pack_e4m3x4(h2f_lo_mul(r[0], inv_in), h2f_hi_mul(r[0], inv_in), h2f_lo_mul(r[1], inv_in),
                                         h2f_hi_mul(r[1], inv_in));
@@ -837,36 +861,36 @@ __device__ __forceinline__ void fb_expand(const BodyFusedArgs& P, BodyTileF t, c
   }
 }
 
-template <int MODE, typename Tin, int TT = BodyFusedCfg<MODE>::T>
+// Frame-input expand: the skip residual of each core pixel is the one compress kept (skip_slot).
+template <int MODE, int TT = BodyFusedCfg<MODE>::T>
 __device__ __forceinline__ void fb_expand_rgb(const BodyFusedArgs& P, BodyTileF t, const unsigned char* src,
                                               const float* cst, const typename BodyFusedCfg<MODE>::Frag* fr,
-                                              const h8 (&pf)[2], const Analysis& an, RgbStage<Tin>& stN,
-                                              unsigned char* slice, int* counter, int wave, int lane) {
+                                              int* counter, int wave, int lane) {
   typedef BodyFusedCfg<MODE, TT> C;
   constexpr int S = C::T, N = S * S, G = (N + 15) / 16;
   static_assert(N % 16 == 0, "expand groups cover whole tiles");
   const int n = lane & 15, g = lane >> 4;
-  const Tin* frame = reinterpret_cast<const Tin*>(P.frames) + (size_t)t.b * 3 * P.H * P.W;
   for (int pg = wave, next; pg < G; pg = next) {
-    stage_store<Tin>(stN, reinterpret_cast<float*>(slice), an, lane);
-    features_to_slice(slice, group_geom(t.y0, t.x0, S, pg).m, an, lane);
     next = claim_group(counter, lane);
-    if (next < G) stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, S, next), P, lane);
     const int q = pg * 16 + n;
     const int r = q / S, c = q - r * S;
     const int ly = t.y0 + r, lx = t.x0 + c;
+    const bool store = ly < P.Hl && lx < P.Wl;
+    // the kept skip values first (in flight during the MFMAs); pixels past the low grid read
+    // the grid's last pixel and store nothing
+    const int lyc = min(ly, P.Hl - 1), lxc = min(lx, P.Wl - 1);
+    u4 kept[4];
+#pragma unroll
+    for (int ph = 0; ph < 4; ++ph) kept[ph] = *reinterpret_cast<const u4*>(skip_slot(P, t.b, lyc, lxc, ph, g));
     typename C::Acc acc[8];
     expand_mma<MODE>(src, q, [&](int i) { return fr[i * 64 + lane]; }, g, acc);
-    const f4 bs0 = *reinterpret_cast<const f4*>(cst + kCstProject + 4 * g);
-    const f4 bs1 = *reinterpret_cast<const f4*>(cst + kCstProject + 16 + 4 * g);
     u2 sk[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const u4 r4 = project_phase(slice, pf, bs0, bs1, k, lane);
-      sk[k] = u2{r4[0], r4[1]};                      // output tile k: phase k, channels 4g..4g+3
-      sk[k + 4] = u2{r4[2], r4[3]};                  // output tile k + 4: channels 16 + 4g..
+      sk[k] = u2{kept[k][0], kept[k][1]};            // output tile k: phase k, channels 4g..4g+3
+      sk[k + 4] = u2{kept[k][2], kept[k][3]};        // output tile k + 4: channels 16 + 4g..
     }
-    if (ly < P.Hl && lx < P.Wl) expand_store<MODE>(P, t.b, ly, lx, cst, acc, sk, g);
+    if (store) expand_store<MODE>(P, t.b, ly, lx, cst, acc, sk, g);
   }
 }
 
@@ -962,7 +986,9 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   } else {
     fb_compress<MODE, TT>(P, t, bufA, cst, Fc, rawN, wave, lane);
   }
-  if constexpr (RGB) {                                 // expand weights: in flight during the barrier
+  if constexpr (RGB) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // kept skip values stored before the barrier
+    // expand weights: in flight during the barrier
     const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[5], C::FragBytes);
     const int voff = fresh(tid) * 16;
 #pragma unroll
@@ -978,6 +1004,7 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
       stage_fetch<Tin>(stN, frame, group_geom(t.y0 - 4, t.x0 - 4, C::S0, wave), P, fresh(lane));
       lds_barrier();
       fb_compress_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters, wave, lane);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // its kept skip values are stored too
       // the weights are loaded again rather than kept live through that compress
       const __amdgpu_buffer_rsrc_t r = frag_rsrc(P.frag[5], C::FragBytes);
       const int voff = fresh(tid) * 16;
@@ -1002,19 +1029,10 @@ __device__ __forceinline__ void body_tile(const BodyFusedArgs& P, int tidx) {
   const FragSet<MODE, 2 * C::NKg> F4 = load_frags<MODE, 2 * C::NKg>(P.frag[4], gf, lane);
   lds_barrier();
   fb_grouped<MODE, 4, TT>(P, t, bufB, bufA, cst, F4, counters + 8 + (wave & 1), wave, lane);
-  // frame input: the first expand group's RGB loads are issued with the expand weights (its
-  // slice in the second buffer is written only after the barrier that ends the bottleneck)
-  if constexpr (RGB) {
-    stage_fetch<Tin>(stN, frame, group_geom(t.y0, t.x0, C::T, wave), P, fresh(lane));
-    // the project fragments are loaded again rather than kept live through the grouped layers
-    const int l = fresh(lane);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) pf[i] = reinterpret_cast<const h8*>(P.pfrag)[i * 64 + l];
-  }
   FragSet<MODE, 8 * C::NKe> Fe;
   if constexpr (!RGB) Fe = load_frags<MODE, 8 * C::NKe>(P.frag[5], 0, lane);
   lds_barrier();
-  if constexpr (RGB) fb_expand_rgb<MODE, Tin, TT>(P, t, bufA, cst, fr, pf, an, stN, slice, counters + 1, wave, lane);
+  if constexpr (RGB) fb_expand_rgb<MODE, TT>(P, t, bufA, cst, fr, counters + 1, wave, lane);
   else fb_expand<MODE, TT>(P, t, bufA, cst, Fe, wave, lane);
 }
 
