@@ -352,7 +352,8 @@ struct Geometry {
   int body_split = 0;              // frame-input body: leading frames on 24x24 tiles, the rest on 16x16
   int body_cols24 = 0;             // frame-input body: > 0: low columns [0, body_cols24) on 24x24 tiles, the rest on 16x16
   int body_rows16 = 0;             // FP16 policy body: low rows on 16x16 tiles, the rest on 8x8
-  int body_xc_tile = 0;            // frame-input body with the compress exchange: its tile side (0: off)
+  int body_xc_tile = 0;            // frame-input body with the compress exchange: its tile code (0: off)
+  int body_xc_frames = 0;          // ... in launches of this many whole frames
   int cus = 0;                     // compute units of the device
   struct Grids { int project, compress, grouped, expand, refine, head, fused; } grid{};
 
@@ -830,12 +831,21 @@ static Geometry make_geometry(int mode, bool project_precise, int cus, int batch
   g.body_cols24 = plan.cols24;
   g.body_rows16 = (flags & AEISU_FLAG_BODY_TILE24) ? g.Hl : body_fused_row_split(mode, batch, g.Hl, g.Wl, cus);
   g.cus = cus;
-  // compress exchange: a whole-frame launch of one tile side whose tiles all fit on the device at once
-  // (one block per CU)
-  if (g.fused_rgb && !(flags & AEISU_FLAG_BODY_NO_EXCHANGE) && plan.cols24 == 0 &&
-      (plan.frames24 == batch || plan.frames24 == 0)) {
-    const int tile = plan.frames24 == batch ? 24 : 16;
-    if (body_fused_num_tiles(mode, batch, g.Hl, g.Wl, tile) <= cus) g.body_xc_tile = tile;
+  // compress exchange: a whole-batch launch of one tile side whose tiles all fit on the device at
+  // once (one block per CU), else launches of whole frames where they beat the plan without it
+  if (g.fused_rgb && !(flags & AEISU_FLAG_BODY_NO_EXCHANGE)) {
+    if (plan.cols24 == 0 && (plan.frames24 == batch || plan.frames24 == 0)) {
+      const int tile = plan.frames24 == batch ? 24 : 16;
+      if (body_fused_num_tiles(mode, batch, g.Hl, g.Wl, tile) <= cus) {
+        g.body_xc_tile = tile;
+        g.body_xc_frames = batch;
+      }
+    }
+    if (!g.body_xc_tile && batch > 1) {
+      const BodyXcPlan xp = body_fused_xc_plan(mode, batch, g.Hl, g.Wl, cus, flags & AEISU_FLAG_BODY_TILE24);
+      g.body_xc_tile = xp.tile;
+      g.body_xc_frames = xp.frames;
+    }
   }
   g.grid.fused = clamp_grid(fused_num_tiles(g.in_fp32, batch, height, width, g.Hq, g.Wq, g.py, g.px), 1, cus);
   return g;
@@ -881,10 +891,19 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     const BodySrc src = g.in_fp32 ? BodySrc::Frames32 : BodySrc::Frames16;
     const int k = g.body_split;
     if (g.body_xc_tile) {                          // compress exchange between neighbouring tiles
-      P.xbuf = static_cast<unsigned char*>(sc.xbuf);
-      P.xflags = sc.xflags;
       P.xspins = (g.flags & AEISU_FLAG_BODY_EXCHANGE_FALLBACK) ? 0 : kExchangePolls;
-      check_hip(launch_body_fused_xc(m, src, P, g.batch, g.body_xc_tile, g.cus, s), "fused body launch");
+      // launches of whole frames, each with its own part of the exchange tensor and counters
+      const int per_frame = body_fused_num_tiles(m, 1, g.Hl, g.Wl, g.body_xc_tile);
+      const size_t in_frame = size_t(3) * g.H * g.W * (g.in_fp32 ? 4 : 2);
+      for (int f0 = 0; f0 < g.batch; f0 += g.body_xc_frames) {
+        BodyFusedArgs Q = P;
+        Q.frames = static_cast<const char*>(P.frames) + size_t(f0) * in_frame;
+        Q.work = P.work + size_t(f0) * g.Hq * g.Wq * 32;
+        Q.xbuf = static_cast<unsigned char*>(sc.xbuf) + size_t(f0) * g.Hl * g.Wl * 64;
+        Q.xflags = sc.xflags + size_t(f0) * per_frame;
+        check_hip(launch_body_fused_xc(m, src, Q, std::min(g.body_xc_frames, g.batch - f0), g.body_xc_tile, g.cus, s),
+                  "fused body launch");
+      }
     } else if (g.body_cols24 > 0) {                       // right-hand columns on 16x16 tiles
       BodyFusedArgs Q = P;
       P.col0 = 0;
@@ -1025,7 +1044,8 @@ static std::string startup_report(const Runtime& rt) {
     << " packed=" << g.Wq << 'x' << g.Hq << " low=" << g.Wl << 'x' << g.Hl << " source_pad=" << g.px << ','
     << g.py << " io=" << (g.in_fp32 ? "f32" : "f16") << '/' << (g.out_fp32 ? "f32" : "f16")
     << " body_tiles24_frames=" << g.body_split << " body_tiles24_cols=" << g.body_cols24
-    << " body_exchange_tile=" << g.body_xc_tile << " weights_bytes=" << rt.w->bytes()
+    << " body_exchange_tile=" << g.body_xc_tile << " body_exchange_frames=" << g.body_xc_frames
+    << " weights_bytes=" << rt.w->bytes()
     << " scratch_bytes=" << rt.scratch_bytes() << " static_scratch_bytes=" << kNoAllocScratchBytes
     << " shared_model_users=" << rt.model.use_count();
   return r.str();
@@ -1082,7 +1102,7 @@ static void enqueue_noalloc(const Runtime& rt, int batch, int height, int width,
                           "kernels on FP32 activations (use aeisu_upscale_async)");
   Geometry g = make_geometry(rt.mode, rt.w->project_precise, rt.model->cu_count, batch, height, width, in_layout,
                              out_layout, 0);
-  g.body_xc_tile = 0;                              // the exchange needs its own zeroed counters
+  g.body_xc_tile = g.body_xc_frames = 0;           // the exchange needs its own zeroed counters
   auto up = [](size_t n) { return (n + 255) & ~size_t(255); };
   const size_t need = 256 + up(g.skip_bytes()) + up(g.work_bytes());
   if (need > kNoAllocScratchBytes)

@@ -1088,11 +1088,12 @@ static double pair_makespan(long n1, double c1, long n2, double c2, int cus) {
 //    16x16 tiles.  Where a frame's last 24-wide tile column is mostly past the frame (540p: 248
 //    low columns, 8 in the eleventh tile column), 16x16 tiles cover it for less, and a batch that
 //    needed a third round of 24x24 tiles (540p x 8: 528 tiles on 256 CUs) fits in about two.
-BodyPlan body_fused_plan(int mode, int batch, int Hl, int Wl, int cus) {
+static BodyPlan plan_with_cost(int mode, int batch, int Hl, int Wl, int cus, double& best) {
   BodyPlan best_plan{batch, 0};
+  best = pair_makespan(body_fused_num_tiles(mode, batch, Hl, Wl, 24), 1.0, 0, 0.0, cus);
   if (mode == 0 || cus <= 0) return best_plan;
   const long t24 = body_fused_num_tiles(mode, 1, Hl, Wl, 24), t16 = body_fused_num_tiles(mode, 1, Hl, Wl, 16);
-  double best = -1.0;
+  best = -1.0;
   for (int k = batch; k >= 0; --k) {
     const double cost = pair_makespan(t24 * k, 1.0, t16 * (batch - k), 0.6, cus);
     if (best < 0.0 || cost < 0.99 * best) {
@@ -1110,6 +1111,29 @@ BodyPlan body_fused_plan(int mode, int batch, int Hl, int Wl, int cus) {
     }
   }
   return best_plan;
+}
+BodyPlan body_fused_plan(int mode, int batch, int Hl, int Wl, int cus) {
+  double cost;
+  return plan_with_cost(mode, batch, Hl, Wl, cus, cost);
+}
+
+// Compress exchange in launches of whole frames on 24x24 tiles, for batches whose tiles outnumber
+// the CUs: each launch's tiles all fit on the device at once, so a launch takes about one tile's
+// time, and a tile with the exchange takes kGain of one without it (measured, bench events: Mixed
+// 1080p 65.8 -> 61.6 us; INT8 none left once its compress got cheaper, 1080p x 2 104.0 against
+// 105.8 us with the exchange).  Taken where the launches beat body_fused_plan's simulated schedule
+// without the exchange (in 24x24 tile units), or with tile24_only, the single 24x24 launch.
+BodyXcPlan body_fused_xc_plan(int mode, int batch, int Hl, int Wl, int cus, bool tile24_only) {
+  const double kGain = mode == 3 ? 0.94 : 1.0;
+  BodyXcPlan none{0, 0};
+  if (mode == 0 || cus <= 0) return none;
+  double base;
+  if (tile24_only) base = pair_makespan(body_fused_num_tiles(mode, batch, Hl, Wl, 24), 1.0, 0, 0.0, cus);
+  else plan_with_cost(mode, batch, Hl, Wl, cus, base);
+  const int frames = std::min(batch, cus / body_fused_num_tiles(mode, 1, Hl, Wl, 24));
+  if (frames < 1) return none;
+  const int launches = (batch + frames - 1) / frames;
+  return launches * kGain < 0.99 * base ? BodyXcPlan{24, frames} : none;
 }
 
 // FP16 policy: the same trade between 16x16 tiles and 8x8 tiles (compress region 16^2 against

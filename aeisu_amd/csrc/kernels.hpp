@@ -76,6 +76,13 @@ struct BodyPlan {
   int frames24, cols24;
 };
 BodyPlan body_fused_plan(int mode, int batch, int Hl, int Wl, int cus);
+// Frame-input body with the compress exchange in launches of `frames` whole frames on tiles of side
+// `tile` (tile 0: the launches do not fit or do not pay); tile24_only: compared with the single
+// 24x24-tile launch instead of the body plan.
+struct BodyXcPlan {
+  int tile, frames;
+};
+BodyXcPlan body_fused_xc_plan(int mode, int batch, int Hl, int Wl, int cus, bool tile24_only);
 // FP16 policy (skip input): low rows [0, R) on 16x16 tiles, the rest on 8x8 tiles; returns R
 int body_fused_row_split(int mode, int batch, int Hl, int Wl, int cus);
 hipError_t body_fused_prepare();

@@ -346,7 +346,8 @@ def measure(args, config: int, size=None, batch=None, precision=None, cpu_budget
 
     # the body's launch shape as configured (tile sides, halo exchange) from the startup report
     report = dict(kv.split("=", 1) for kv in hd.report().split() if "=" in kv)
-    body_launch = {k: int(report[k]) for k in ("body_tiles24_frames", "body_tiles24_cols", "body_exchange_tile")
+    body_launch = {k: int(report[k]) for k in ("body_tiles24_frames", "body_tiles24_cols", "body_exchange_tile",
+                                               "body_exchange_frames")
                    if k in report}
 
     fps = B * 1000.0 / ms_per_step

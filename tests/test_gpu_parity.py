@@ -141,11 +141,12 @@ def test_fused_equals_unfused(mixed_model, fp16_model, int8_model, fp8mma_model,
     must reproduce the per-layer path bit for bit in every policy, including odd padding offsets
     (70x102 -> py = px = 29), frames narrower than one tile row and low grids that are not a multiple
     of the body tile (37x333, 200x72 in a batch of 3), with the body tiles these shapes select (16x16 for
-    the small frames; 540p x 8 splits into 7 frames on 24x24 and 1 on 16x16 tiles, two launches) and with
-    24x24 tiles forced; each with the compress exchange between neighbouring tiles (the default where a
-    launch's tiles all fit on the device at once; 1080p x 2 has more tiles than CUs and runs without it),
-    without it, and with every tile taking the exchange's fallback (computing its halo ring itself, as
-    when its neighbours do not arrive in time)."""
+    the small frames; 540p x 8: every frame's low columns 0..215 on 24x24 tiles and the rest on 16x16
+    tiles in one launch) and with 24x24 tiles forced (the Mixed policy's 540p x 8 then runs the exchange
+    in launches of 3, 3 and 2 frames); each with the compress exchange between neighbouring tiles (the
+    default where a launch's tiles all fit on the device at once; the Mixed policy's 1080p x 2 runs it
+    one frame per launch), without it, and with every tile taking the exchange's fallback (computing its
+    halo ring itself, as when its neighbours do not arrive in time)."""
     from aeisu_amd import _lib as L
     say(f"case: fused vs unfused {b}x3x{h}x{w} fp32={fp32}")
     dt = torch.float32 if fp32 else torch.float16
@@ -269,22 +270,27 @@ def test_full_size_1080p_properties(mixed_model, int8_model, fp16_model, fp8mma_
 
 
 def test_body_exchange_selection(mixed_model, int8_model):
-    """The compress exchange is configured where a whole-frame body launch fits on the device (1080p,
-    720p and 540p at batch 1), not where the tiles outnumber the CUs (1440p, 540p x 8), not with the
-    opt-out flag, and its buffers (64 bytes per low pixel, a counter per tile) are counted in the
-    persistent bytes."""
+    """The compress exchange is configured where a whole-batch body launch fits on the device (1080p,
+    720p and 540p at batch 1); for the Mixed policy also in launches of whole frames where those beat
+    the plan without it (1080p x 2: one frame per launch); not where a frame's tiles outnumber the CUs
+    (1440p) or the launches would not pay (540p x 8: three frames per launch; INT8 1080p x 2, whose
+    tiles gain nothing from it), not with the opt-out flag; and its buffers (64 bytes per low pixel, a
+    counter per tile) are counted in the persistent bytes."""
     from aeisu_amd import _lib as L
     say("case: compress-exchange selection")
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     for model in (mixed_model, int8_model):
-        for b, h, w, flags, expect in ((1, 1080, 1920, 0, 24), (1, 540, 960, 0, 16), (8, 540, 960, 0, 0),
-                                       (1, 1440, 2560, 0, 0), (1, 1080, 1920, L.FLAG_BODY_NO_EXCHANGE, 0)):
+        mixed = model is mixed_model
+        for b, h, w, flags, expect, frames in (
+                (1, 1080, 1920, 0, 24, 1), (1, 540, 960, 0, 16, 1), (2, 1080, 1920, 0, 24 if mixed else 0, 1 if mixed else 0),
+                (8, 540, 960, 0, 0, 0), (1, 1440, 2560, 0, 0, 0), (1, 1080, 1920, L.FLAG_BODY_NO_EXCHANGE, 0, 0)):
             hd = model.handle(b, h, w, torch.float16, torch.float16, flags)
             report = hd.report()
             tile = int(report.split("body_exchange_tile=")[1].split()[0])
-            say(f"  {model.precision} {b}x{h}x{w} flags={flags}: exchange tile {tile}")
+            per_launch = int(report.split("body_exchange_frames=")[1].split()[0])
+            say(f"  {model.precision} {b}x{h}x{w} flags={flags}: exchange tile {tile}, {per_launch} frames per launch")
             if cus >= 256:
-                assert tile == expect
+                assert (tile, per_launch) == (expect, frames)
             if tile == 0:
                 continue
             off = model.handle(b, h, w, torch.float16, torch.float16, flags | L.FLAG_BODY_NO_EXCHANGE)
