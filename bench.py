@@ -396,7 +396,7 @@ def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are out of scope "
-              "(frames shard across GPUs with no exchange, see DESIGN.md)", file=sys.stderr)
+              "(frames would shard across GPUs, one runtime per GPU, with no exchange)", file=sys.stderr)
         sys.exit(2)
     if args.table:
         rows = []
