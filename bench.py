@@ -200,6 +200,12 @@ def measure(args, config: int, size=None, batch=None, precision=None, cpu_budget
         return 1000 * (time.perf_counter() - t0) / args.steps
 
     model.run(pool[0], out=outs[0], flags=run_flags)         # finite check once, outside timing
+    # The per-frame graphs are captured before the clock warm-up: capturing and instantiating them
+    # leaves the GPU idle for long enough that it lowers its clocks, and the frames timed right after
+    # ran up to 12 % slower (one box: 137.8 against 123.4 us per frame, recovering over about 60 frames).
+    for j in range(len(pool)):
+        step(j, True)
+    torch.cuda.synchronize()
     # The GPU raises its clocks only after some milliseconds of load: W warm-up frames (~1 ms at
     # W = 5) leave the timed frames at a lower clock than a serving loop runs at (0.165-0.169 against
     # 0.143 ms per 1080p frame on one box).  Frames are run untimed for --clock-warmup seconds first.
@@ -210,8 +216,8 @@ def measure(args, config: int, size=None, batch=None, precision=None, cpu_budget
             step(n_warm, False)
             n_warm += 1
         torch.cuda.synchronize()
-    graph_ms = timed(True)
     eager_launch_ms = timed(False)
+    graph_ms = timed(True)
     graph = args.graph
     ms_per_step = graph_ms if graph else eager_launch_ms
     log(f"bench: {eager_launch_ms:.4f} ms/step eager, {graph_ms:.4f} ms/step graph replay "
