@@ -24,9 +24,13 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-ta
 
 # Per-source compiler options.  The fused head is latency-bound (four waves per SIMD); LLVM's
 # iterative ILP scheduler orders its instructions for latency within the same 128-VGPR budget
-# (no spills) and took 0.5 us off it at 1080p (A/B on one box); the body and the other kernels keep
-# the default scheduler (max-ilp / max-memory-clause measured no better there).
-FILE_FLAGS = {"k_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
+# (no spills) and took 0.5 us off it at 1080p (A/B on one box).  The frame-input body (Mixed,
+# FP8-MFMA, INT8) gains from it too (1080p Mixed 61.9 -> 60.1 us, INT8 540p x 8 111.2 -> 109.4 us,
+# no spills), the FP16 policy's skip-input body (k_body_fused_fp16.hip) does not (71.4 -> 73.6 us)
+# and keeps the default scheduler, as the other kernels do (max-ilp / max-memory-clause measured no
+# better there).
+FILE_FLAGS = {"k_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+              "k_body_fused.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]}
 
 
 def sources():
