@@ -385,20 +385,21 @@ __device__ __forceinline__ GroupGeom group_geom(int oy, int ox, int S, int pg) {
   return gg;
 }
 
-// Raw staged values in flight (FP16 frames: two per register).
+// Raw staged values in flight, one 32-bit word each (FP16 frames: zero-extended).  They pass
+// through an empty asm statement before stage_store reads them: packed two FP16 values per
+// register, the compiler waited for the loads right after issuing them.
 template <typename Tin>
-struct RgbStage;
-template <>
-struct RgbStage<float> {
-  float v[kStageLoads];
-  __device__ __forceinline__ void set(int e, float x) { v[e] = x; }
-  __device__ __forceinline__ float get(int e) const { return v[e]; }
-};
-template <>
-struct RgbStage<_Float16> {
-  h2 v[(kStageLoads + 1) / 2];
-  __device__ __forceinline__ void set(int e, _Float16 x) { v[e >> 1][e & 1] = x; }
-  __device__ __forceinline__ float get(int e) const { return (float)v[e >> 1][e & 1]; }
+struct RgbStage {
+  unsigned v[kStageLoads];
+  __device__ __forceinline__ void set(int e, unsigned x) { v[e] = x; }
+  __device__ __forceinline__ float get(int e) const {
+    if constexpr (sizeof(Tin) == 2) return (float)__builtin_bit_cast(_Float16, (unsigned short)v[e]);
+    else return __builtin_bit_cast(float, v[e]);
+  }
+  __device__ __forceinline__ void settle() {
+#pragma unroll
+    for (int e = 0; e < kStageLoads; ++e) asm volatile("" : "+v"(v[e]));
+  }
 };
 // Lane L takes stage column L (rows 0..5, value c * kSR + row) and, for L < 24, the pixel (row
 // L >> 2, column 64 + (L & 3)) (values 3 kSR + c).  Loads are unconditional with clamped
@@ -410,9 +411,9 @@ __device__ __forceinline__ int stage_src_x(const GroupGeom& gg, int j, int px, i
   return min(max(X - px, 0), W - 1);
 }
 template <typename Tin>
-__device__ __forceinline__ Tin stage_load(__amdgpu_buffer_rsrc_t rs, int off, int soff) {
-  if constexpr (sizeof(Tin) == 2) return __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, off, soff, 0));
-  else return __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, off, soff, 0));
+__device__ __forceinline__ unsigned stage_load(__amdgpu_buffer_rsrc_t rs, int off, int soff) {
+  if constexpr (sizeof(Tin) == 2) return (unsigned)__builtin_amdgcn_raw_buffer_load_b16(rs, off, soff, 0);
+  else return __builtin_amdgcn_raw_buffer_load_b32(rs, off, soff, 0);
 }
 template <typename Tin>
 __device__ __forceinline__ void stage_fetch(RgbStage<Tin>& st, const Tin* __restrict__ frame, const GroupGeom& gg,
@@ -440,7 +441,8 @@ __device__ __forceinline__ void stage_fetch(RgbStage<Tin>& st, const Tin* __rest
   }
 }
 template <typename Tin>
-__device__ __forceinline__ void stage_store(const RgbStage<Tin>& st, float* stg, const Analysis& an, int lane) {
+__device__ __forceinline__ void stage_store(RgbStage<Tin>& st, float* stg, const Analysis& an, int lane) {
+  st.settle();
   float* rgb = stg + kSPlane;
 #pragma unroll
   for (int row = 0; row < kSR; ++row) {

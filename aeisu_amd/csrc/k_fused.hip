@@ -271,11 +271,13 @@ __device__ __forceinline__ void produce(const unsigned char* smem, const unsigne
 // The RGB tile of the next tile is loaded into registers as raw frame values and converted
 // only when it is stored to LDS: converting at load time makes the compiler wait for each
 // load right away, which would expose the memory latency instead of hiding it behind the
-// current tile.  Loads are unconditional (indices clamped into the tile) so they are not
-// split into branches either.
+// current tile.  The raw values are held as zero-extended 32-bit words and pass through an
+// empty asm statement at the store, so that the compiler cannot pack two FP16 channels into
+// one register (and wait for both loads) right after the loads.  Loads are unconditional
+// (indices clamped into the tile) so they are not split into branches either.
 template <typename Tin, typename LY>
 struct RgbRegs {
-  Tin v[LY::RgbPer][3];
+  unsigned v[LY::RgbPer][3];
 };
 template <typename Tin, typename LY>
 __device__ __forceinline__ void rgb_fetch(RgbRegs<Tin, LY>& r, const Tin* __restrict__ src, FusedTile t,
@@ -295,20 +297,27 @@ __device__ __forceinline__ void rgb_fetch(RgbRegs<Tin, LY>& r, const Tin* __rest
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
       if constexpr (sizeof(Tin) == 2)
-        r.v[k][c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, o, c * plane, 0));
+        r.v[k][c] = (unsigned)__builtin_amdgcn_raw_buffer_load_b16(rs, o, c * plane, 0);
       else
-        r.v[k][c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, o, c * plane, 0));
+        r.v[k][c] = __builtin_amdgcn_raw_buffer_load_b32(rs, o, c * plane, 0);
     }
   }
 }
-__device__ __forceinline__ void rgb_put(h4* d, _Float16 a, _Float16 b, _Float16 c) { *d = h4{a, b, c, (_Float16)0.0f}; }
-__device__ __forceinline__ void rgb_put(float4* d, float a, float b, float c) { *d = make_float4(a, b, c, 0.f); }
+// FP16: (r, g) in the first dword, (b, 0) in the second (the loads zero-extend); FP32: the bits.
+__device__ __forceinline__ void rgb_put(h4* d, unsigned a, unsigned b, unsigned c) {
+  *reinterpret_cast<u2*>(d) = u2{__builtin_amdgcn_perm(b, a, 0x05040100u), c};
+}
+__device__ __forceinline__ void rgb_put(float4* d, unsigned a, unsigned b, unsigned c) {
+  *d = make_float4(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b), __builtin_bit_cast(float, c), 0.f);
+}
 template <typename Tin, typename Rgb, typename LY>
 __device__ __forceinline__ void rgb_store(const RgbRegs<Tin, LY>& r, Rgb* lds_rgb, int ctid) {
 #pragma unroll
   for (int k = 0; k < LY::RgbPer; ++k) {
     const int q = ctid + LY::ConsumerThreads * k;
-    if (q < LY::RPos) rgb_put(lds_rgb + q, r.v[k][0], r.v[k][1], r.v[k][2]);
+    unsigned a = r.v[k][0], b = r.v[k][1], c = r.v[k][2];
+    asm volatile("" : "+v"(a), "+v"(b), "+v"(c));
+    if (q < LY::RPos) rgb_put(lds_rgb + q, a, b, c);
   }
 }
 
@@ -341,13 +350,21 @@ __device__ __forceinline__ void fstore_pair<float>(__amdgpu_buffer_rsrc_t r, uns
 // (every LDS address stays inside the tile buffers), so the row is one basic block the
 // scheduler can interleave; chunks or lanes past the frame edge only lose their stores.
 // QC: A23 is unused and BC holds the lane group's FP32 base per row tile; otherwise BC is unused.
-template <typename Tout, typename Rgb, bool QC>
+// `mid` is called once per row, after the second chunk's arithmetic and before any output store
+// is issued (at once for a row outside the frame): the caller stores the next tile's RGB there,
+// so that waiting for its loads does not also wait for this row's output stores, which are
+// counted by the same counter.
+template <typename Tout, typename Rgb, bool QC, typename Mid>
 __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const Rgb* lds_rgb, Tout* __restrict__ out,
                                             FusedTile t, const FusedGeom& G, int r, int lane, const h8 (&A1)[7],
-                                            const h8 (&A23)[7], const f4 (&BC)[7], const unsigned ones, float& chk) {
+                                            const h8 (&A23)[7], const f4 (&BC)[7], const unsigned ones, float& chk,
+                                            Mid&& mid) {
   const int n = lane & 15, g = lane >> 4;
   const int y = 2 * t.qy0 + r - G.py;
-  if (y < 0 || y >= G.H) return;                      // wave-uniform
+  if (y < 0 || y >= G.H) {                            // wave-uniform
+    mid();
+    return;
+  }
   const size_t oplane = (size_t)4 * G.H * G.W;
   const __amdgpu_buffer_rsrc_t ob = frame_rsrc(out + (size_t)t.b * 3 * oplane, 3 * oplane * sizeof(Tout));
   const _Float16* mrow = reinterpret_cast<const _Float16*>(lds_meta) + (r >> 1) * kFQW * kFMPix;
@@ -417,6 +434,7 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const unsigned off01 = inside ? o0 + (unsigned)(c01 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
     const unsigned off2 = inside && c01 == 0 ? o0 + (unsigned)(2 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
     if constexpr (std::is_same<Tout, float>::value) {
+      if (j == 0) mid();
       fstore_pair<Tout>(ob, off01, c01 ? left[1] : left[0], c01 ? right[1] : right[0]);
       fstore_pair<Tout>(ob, off2, left[2], right[2]);
     } else {
@@ -426,6 +444,7 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
       so01[j] = off01;
       so2[j] = off2;
       if (j & 1) {
+        if (j == 1) mid();
 #pragma unroll
         for (int k = j - 1; k <= j; ++k) __builtin_amdgcn_raw_buffer_store_b32(sv01[k], ob, (int)so01[k], 0, kStoreNonTemporal);
 #pragma unroll
@@ -497,6 +516,14 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
     if constexpr (QC) BC[q] = basec[g * 7 + q];
     else A23[q] = bankA[(7 + q) * 64 + lane];
   }
+  // The bank fragments are used first inside the tile loop.  Waiting for them here, on every
+  // path into the loop, keeps the compiler from placing waits for them inside the loop, where
+  // they would also wait for the RGB prefetch of the next tile.
+#pragma unroll
+  for (int q = 0; q < 7; ++q) {
+    if constexpr (QC) asm volatile("" ::"v"(A1[q]), "v"(BC[q]));
+    else asm volatile("" ::"v"(A1[q]), "v"(A23[q]));
+  }
   const unsigned ones = g == 0 ? 0x3C003C00u : 0u;  // FP16 (1, 1) in B slots 4, 5 of lane group 0
   float chk = 0.f;
   const int t0 = tile_of(0, G.num_tiles);
@@ -517,10 +544,13 @@ __device__ __forceinline__ void consumer_main(unsigned char* smem, const Tin* __
     const int cur = it & 1, nxt = cur ^ 1;
     RgbRegs<Tin, LY> rr;
     if (tn < G.num_tiles) rgb_fetch<Tin, LY>(rr, src, fused_tile<LY::QH>(tn, G), G, ctid);
+    // the next tile's RGB buffer was last read before the previous barrier
     consume_row<Tout, Rgb, QC>(smem + LY::OffMeta + cur * LY::SizeMeta,
                                reinterpret_cast<const Rgb*>(smem + LY::OffRgb + cur * LY::SizeRgb), out,
-                               fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, BC, ones, chk);
-    if (tn < G.num_tiles) rgb_store<Tin, Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
+                               fused_tile<LY::QH>(tc, G), G, row, lane, A1, A23, BC, ones, chk, [&]() {
+                                 if (tn < G.num_tiles)
+                                   rgb_store<Tin, Rgb, LY>(rr, reinterpret_cast<Rgb*>(smem + LY::OffRgb + nxt * LY::SizeRgb), ctid);
+                               });
     lds_barrier();
   }
   if (nonfinite && __ballot(chk != chk) != 0ull && lane == 0) atomicOr(nonfinite, 1u);
