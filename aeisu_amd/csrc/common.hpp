@@ -189,24 +189,27 @@ __device__ __forceinline__ unsigned pack_h2_clamp01(float a, float b) {
   asm("v_cvt_pk_f16_f32 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
+// gfx950's v_pk_minimum3_f16: per half, the IEEE 754-2019 minimum of three FP16 values (a NaN
+// operand gives a quiet NaN, unlike v_pk_min_f16, which returns the other operand).
+__device__ __forceinline__ unsigned pk_minimum3_h16(unsigned a, unsigned b, unsigned c) {
+  unsigned r;
+  asm("v_pk_minimum3_f16 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 // Two FP16 coefficients (one dword) -> (u, w) with TransferCoefficient(v) = u + 0.05 w
 // (reference: |v| <= 2 ? v : sign(v) min(2.5, 2 + 0.05 (|v| - 2))), both exact in FP16:
-// u = sign(v) min(|v|, 2), w = sign(v) min(max(|v| - 2, 0), 10); a NaN v gives a quiet NaN u.
-// Integer min on the magnitude bits, one exact FP16 subtraction, and an unsigned
-// multiply-add whose clamp turns any NaN magnitude into 0xFFFF (all 65536 codes checked
-// against the value formula).
+// u = sign(v) min(|v|, 2), w = sign(v) min(max(|v| - 2, 0), 10); a NaN v gives NaN u and w.
+// u is a NaN-propagating minimum, w an integer min on the magnitude bits (unsigned order is
+// value order for non-negative FP16) and one exact FP16 subtraction.  On gfx950 every code of both
+// halves gives the same u and w as the integer-min form with a saturating NaN fix-up that this
+// replaced (all 65,536 codes, NaN codes to NaN with their sign).
 __device__ __forceinline__ void coef_clamp_split(unsigned v, unsigned& u, unsigned& w) {
   typedef unsigned short us2v __attribute__((ext_vector_type(2)));
-  const us2v m = __builtin_bit_cast(us2v, v & 0x7FFF7FFFu);
-  const us2v um = __builtin_elementwise_min(m, (us2v){0x4000, 0x4000});          // min(|v|, 2)
-  const us2v mc = __builtin_elementwise_min(m, (us2v){0x4A00, 0x4A00});          // min(|v|, 12)
+  const unsigned mb = v & 0x7FFF7FFFu;
+  const unsigned um = pk_minimum3_h16(mb, 0x40004000u, 0x40004000u);             // min(|v|, 2)
+  const us2v mc = __builtin_elementwise_min(__builtin_bit_cast(us2v, mb), (us2v){0x4A00, 0x4A00});  // min(|v|, 12)
   const h2 wm = __builtin_bit_cast(h2, mc) - __builtin_bit_cast(h2, um);         // exact
-  const us2v nanpart = __builtin_elementwise_sub_sat(m, (us2v){0x7C00, 0x7C00});  // > 0 only for NaN
-  unsigned ub;
-  asm("v_pk_mad_u16 %0, %1, %2, %3 clamp"
-      : "=v"(ub)
-      : "v"(__builtin_bit_cast(unsigned, nanpart)), "s"(0xFFFFFFFFu), "v"(__builtin_bit_cast(unsigned, um)));
-  u = (ub & 0x7FFF7FFFu) | (v & 0x80008000u);
+  u = (um & 0x7FFF7FFFu) | (v & 0x80008000u);
   w = (__builtin_bit_cast(unsigned, wm) & 0x7FFF7FFFu) | (v & 0x80008000u);
 }
 // Two FP16 coefficients (one dword) -> the clamped coefficients rounded to FP16, for the head of
@@ -215,25 +218,18 @@ __device__ __forceinline__ void coef_clamp_split(unsigned v, unsigned& u, unsign
 //   c = sign(v) min(rne16((|v| - 2) h + 2), 2.5)       otherwise, h = fp16(0.05) = 0.0499877...,
 // one fused rounding (|v| - 2 is exact in FP16 for |v| >= 1); c(+-inf) = +-2.5, a NaN v gives a
 // quiet NaN.  The select is a minimum: rne16((m - 2) h + 2) >= m for m <= 2 and < m above, so
-// c = min(m, t, 2.5) on the magnitude m.  Differs from the FP32 clamp by at most half an FP16
-// ulp of c plus (0.05 - h)(|v| - 2) <= 1.2e-4, only where |v| > 2.
+// c = min(m, t, 2.5) on the magnitude m, one NaN-propagating three-way minimum.  Differs from the
+// FP32 clamp by at most half an FP16 ulp of c plus (0.05 - h)(|v| - 2) <= 1.2e-4, only where
+// |v| > 2.  On gfx950 every code gives the result of the integer-min form with a saturating NaN
+// fix-up that this replaced (all 65,536 codes in both halves).
 __device__ __forceinline__ unsigned coef_clamp_h16(unsigned v) {
-  typedef unsigned short us2v __attribute__((ext_vector_type(2)));
   const unsigned mb = v & 0x7FFF7FFFu;
   const h2 m = __builtin_bit_cast(h2, mb);
   const h2 two = {(_Float16)2.0f, (_Float16)2.0f};
   const h2 h05 = {(_Float16)0.05f, (_Float16)0.05f};
-  // t >= 1.9 (or +inf) for every non-NaN m, so the minima run on the bit patterns (unsigned
-  // order = value order for non-negative FP16), which needs no NaN canonicalisation
-  const us2v t = __builtin_elementwise_min(__builtin_bit_cast(us2v, __builtin_elementwise_fma(m - two, h05, two)),
-                                           (us2v){0x4100, 0x4100});                    // min(., 2.5)
-  const us2v c = __builtin_elementwise_min(__builtin_bit_cast(us2v, mb), t);
-  const us2v nanpart = __builtin_elementwise_sub_sat(__builtin_bit_cast(us2v, mb), (us2v){0x7C00, 0x7C00});
-  unsigned cb;
-  asm("v_pk_mad_u16 %0, %1, %2, %3 clamp"
-      : "=v"(cb)
-      : "v"(__builtin_bit_cast(unsigned, nanpart)), "s"(0xFFFFFFFFu), "v"(__builtin_bit_cast(unsigned, c)));
-  return (cb & 0x7FFF7FFFu) | (v & 0x80008000u);
+  const h2 t = __builtin_elementwise_fma(m - two, h05, two);
+  const unsigned c = pk_minimum3_h16(mb, __builtin_bit_cast(unsigned, t), 0x41004100u);   // min(m, t, 2.5)
+  return (c & 0x7FFF7FFFu) | (v & 0x80008000u);
 }
 __device__ __forceinline__ float h2f_lo(unsigned w) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xFFFFu));

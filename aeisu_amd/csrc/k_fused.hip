@@ -271,10 +271,10 @@ __device__ __forceinline__ void produce(const unsigned char* smem, const unsigne
 // The RGB tile of the next tile is loaded into registers as raw frame values and converted
 // only when it is stored to LDS: converting at load time makes the compiler wait for each
 // load right away, which would expose the memory latency instead of hiding it behind the
-// current tile.  The raw values are held as zero-extended 32-bit words and pass through an
-// empty asm statement at the store, so that the compiler cannot pack two FP16 channels into
-// one register (and wait for both loads) right after the loads.  Loads are unconditional
-// (indices clamped into the tile) so they are not split into branches either.
+// current tile.  The raw values are held as zero-extended 32-bit words and packed at the store
+// by a volatile asm, so that the compiler cannot pack two FP16 channels into one register (and
+// wait for both loads) right after the loads.  Loads are unconditional (indices clamped into the
+// tile) so they are not split into branches either.
 template <typename Tin, typename LY>
 struct RgbRegs {
   unsigned v[LY::RgbPer][3];
@@ -303,9 +303,12 @@ __device__ __forceinline__ void rgb_fetch(RgbRegs<Tin, LY>& r, const Tin* __rest
     }
   }
 }
-// FP16: (r, g) in the first dword, (b, 0) in the second (the loads zero-extend); FP32: the bits.
+// FP16: (r, g) in the first dword, (b, 0) in the second (the loads zero-extend); the packing is a
+// volatile asm so that it stays here.  FP32: the bits.
 __device__ __forceinline__ void rgb_put(h4* d, unsigned a, unsigned b, unsigned c) {
-  *reinterpret_cast<u2*>(d) = u2{__builtin_amdgcn_perm(b, a, 0x05040100u), c};
+  unsigned rg;
+  asm volatile("v_perm_b32 %0, %1, %2, %3" : "=v"(rg) : "v"(b), "v"(a), "s"(0x05040100u));
+  *reinterpret_cast<u2*>(d) = u2{rg, c};
 }
 __device__ __forceinline__ void rgb_put(float4* d, unsigned a, unsigned b, unsigned c) {
   *d = make_float4(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b), __builtin_bit_cast(float, c), 0.f);
@@ -315,9 +318,7 @@ __device__ __forceinline__ void rgb_store(const RgbRegs<Tin, LY>& r, Rgb* lds_rg
 #pragma unroll
   for (int k = 0; k < LY::RgbPer; ++k) {
     const int q = ctid + LY::ConsumerThreads * k;
-    unsigned a = r.v[k][0], b = r.v[k][1], c = r.v[k][2];
-    asm volatile("" : "+v"(a), "+v"(b), "+v"(c));
-    if (q < LY::RPos) rgb_put(lds_rgb + q, a, b, c);
+    if (q < LY::RPos) rgb_put(lds_rgb + q, r.v[k][0], r.v[k][1], r.v[k][2]);
   }
 }
 
