@@ -415,18 +415,10 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const bool inside = (unsigned)x < (unsigned)G.W;
     chk = fmaf(inside ? u[0] + u[1] + u[2] : 0.f, 0.0f, chk);
     // pair phases (TL, TR) and (BL, BR): after the swap lane groups 0 and 1 both hold
-    // (TL, TR), groups 2 and 3 both hold (BL, BR)
-    // (FP16 output: the [0, 1] clamp rides on the packed convert, after the swap)
-    float left[3], right[3];
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-      left[c] = std::is_same<Tout, float>::value ? __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f) : u[c];
-      right[c] = left[c];
-      permlane16_swap(left[c], right[c]);
-    }
-    // both lane groups of a row pair hold the same values: groups 0 / 2 write channel 0 and groups
-    // 1 / 3 channel 1 in one store, then groups 0 / 2 channel 2 (lanes with nothing to write get an
-    // out-of-range offset).  FP16 output: a chunk writes 64 bytes per row and channel, so the
+    // (TL, TR), groups 2 and 3 both hold (BL, BR).
+    // Both lane groups of a row pair then hold the same values: groups 0 / 2 write channel 0 and
+    // groups 1 / 3 channel 1 in one store, then groups 0 / 2 channel 2 (lanes with nothing to write
+    // get an out-of-range offset).  FP16 output: a chunk writes 64 bytes per row and channel, so the
     // stores of chunks j - 1 and j are issued together and fill whole 128-byte lines; with the
     // non-temporal hint, half lines written apart were each sent to memory as a partial line
     // (write traffic 1.44x the output).
@@ -435,13 +427,26 @@ __device__ __forceinline__ void consume_row(const unsigned char* lds_meta, const
     const unsigned off01 = inside ? o0 + (unsigned)(c01 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
     const unsigned off2 = inside && c01 == 0 ? o0 + (unsigned)(2 * oplane * sizeof(Tout)) : 0xFFFFFFFFu;
     if constexpr (std::is_same<Tout, float>::value) {
+      float left[3], right[3];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        left[c] = __builtin_amdgcn_fmed3f(u[c], 0.0f, 1.0f);
+        right[c] = left[c];
+        permlane16_swap(left[c], right[c]);
+      }
       if (j == 0) mid();
       fstore_pair<Tout>(ob, off01, c01 ? left[1] : left[0], c01 ? right[1] : right[0]);
       fstore_pair<Tout>(ob, off2, left[2], right[2]);
     } else {
-      const unsigned p0 = pack_h2_clamp01(left[0], right[0]), p1 = pack_h2_clamp01(left[1], right[1]);
-      sv01[j] = c01 ? p1 : p0;
-      sv2[j] = pack_h2_clamp01(left[2], right[2]);
+      // FP16 output: the lane's own phase is converted (with the [0, 1] clamp) before the swap, so
+      // two swaps move (R, G) and (B, B) as FP16 pairs, and one byte permute per store picks the
+      // left and right halves: (R_l, R_r) or (G_l, G_r) by the lane's channel, and (B_l, B_r).
+      unsigned rgL = pack_h2_clamp01(u[0], u[1]), bbL = pack_h2_clamp01(u[2], u[2]);
+      unsigned rgR = rgL, bbR = bbL;
+      permlane16_swap_u(rgL, rgR);
+      permlane16_swap_u(bbL, bbR);
+      sv01[j] = __builtin_amdgcn_perm(rgR, rgL, c01 ? 0x07060302u : 0x05040100u);
+      sv2[j] = __builtin_amdgcn_perm(bbR, bbL, 0x05040100u);
       so01[j] = off01;
       so2[j] = off2;
       if (j & 1) {
