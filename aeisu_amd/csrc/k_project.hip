@@ -34,8 +34,10 @@ namespace aeisu {
 
 constexpr int kPTW = 32, kPTH = 8;
 constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
-// halves per LDS feature row: 32 features (+ 32 low parts in the FP32-accurate variant) + 8 pad
-template <bool PRECISE> constexpr int kPFeat = PRECISE ? 72 : 40;
+// halves per LDS feature row: 32 features + 8 pad.  The FP32-accurate variant passes its high and
+// low parts through the same rows one after the other, so that the block's LDS (34.8 KB) lets four
+// blocks share a CU instead of three.
+constexpr int kPFeat = 40;
 
 constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
 constexpr int kPRows = 3 * kPLH;                         // region rows of the three channels (54)
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(256) void project_kernel(
     const Tin* __restrict__ src, const h8* __restrict__ wfrag, const float* __restrict__ bias,
     _Float16* __restrict__ skip, Analysis an, int H, int W, int Hq, int Wq, int py, int px, int batch) {
   __shared__ float rgb[3][kPLH][kPLW];
-  __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat<PRECISE>];
+  __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const h8 A0 = wfrag[lane], A1 = wfrag[64 + lane];
@@ -147,26 +149,34 @@ __global__ __launch_bounds__(256) void project_kernel(
       }
     }
     lds_barrier();
+    h8 bop[4], blo[4];
     {
       float f[8][4];
       packed_features(&rgb[0][2 * ty][2 * tx], kPLH * kPLW, kPLW, an, f);
       h8 hi[4], lo[4];
       feature_slices<PRECISE>(f, hi, lo);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        *reinterpret_cast<h8*>(&feat[tid][8 * q]) = hi[q];
-        if constexpr (PRECISE) *reinterpret_cast<h8*>(&feat[tid][32 + 8 * q]) = lo[q];
-      }
-    }
-    // A wave's MFMAs read only the feature rows its own lanes wrote: LDS operations of one wave
-    // execute in order, so a compiler fence (no workgroup barrier) is enough here.
-    asm volatile("" ::: "memory");
-    h8 bop[4], blo[4];
+      for (int q = 0; q < 4; ++q) *reinterpret_cast<h8*>(&feat[tid][8 * q]) = hi[q];
+      // A wave's MFMAs read only the feature rows its own lanes wrote: LDS operations of one wave
+      // execute in order, so compiler fences (no workgroup barrier) are enough here, also for the
+      // low parts written over the high parts once they have been read.
+      asm volatile("" ::: "memory");
 #pragma unroll
-    for (int jg = 0; jg < 4; ++jg) {
-      const int p = wave * 64 + jg * 16 + n;          // pixel index inside the tile
-      bop[jg] = *reinterpret_cast<const h8*>(&feat[p][8 * g]);
-      if constexpr (PRECISE) blo[jg] = *reinterpret_cast<const h8*>(&feat[p][32 + 8 * g]);
+      for (int jg = 0; jg < 4; ++jg) {
+        const int p = wave * 64 + jg * 16 + n;        // pixel index inside the tile
+        bop[jg] = *reinterpret_cast<const h8*>(&feat[p][8 * g]);
+      }
+      if constexpr (PRECISE) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<h8*>(&feat[tid][8 * q]) = lo[q];
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int jg = 0; jg < 4; ++jg) {
+          const int p = wave * 64 + jg * 16 + n;
+          blo[jg] = *reinterpret_cast<const h8*>(&feat[p][8 * g]);
+        }
+      }
     }
     f4 a0[4], a1[4];
 #pragma unroll
