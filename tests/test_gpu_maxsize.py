@@ -4,6 +4,7 @@ aeisu_configure accepts frames up to 8192 x 8192 and rejects larger ones, as the
 runtime test expects (SrcPyrRuntimeTest.cpp:302-303).  At 8192 x 8192 an FP32 output frame is
 3.2 GB and a batch of two FP16 output frames 3.2 GB, so every byte offset the kernels form
 (32-bit raw-buffer offsets inside a frame, 64-bit frame bases) is exercised near its limit.
+The largest batch (1024 frames) is checked against single-frame runs.
 
 The oracle cannot run a whole 8192 x 8192 frame in seconds, so it runs the frame's bottom-right
 corner: the last 384 x 384 input pixels, a sub-frame whose origin is a multiple of 32, so that
@@ -93,6 +94,23 @@ def test_configure_rejects_beyond_maximum(R):
                 model.handle(batch, h, w)
         hd = model.handle(1, MAX, MAX)                        # the maximum itself configures
         assert model.geometry(hd)[:2] == (MAX + 32, MAX + 32)
+    finally:
+        model.close()
+
+
+@pytest.mark.parametrize("precision,artifact", [("mixed", "aeisu_area_mixed_fp8.bin"), ("int8", "aeisu_int8_fp16.pt"),
+                                                ("fp16", "aeisu_area.pt")])
+def test_maximum_batch_equals_single_frames(R, precision, artifact):
+    """The largest batch aeisu_configure accepts (1024 frames, here of 12 x 20 pixels) gives each
+    frame exactly what the frame gives alone."""
+    say(f"case: {precision}, batch 1024 x 3 x 12 x 20")
+    gen = torch.Generator().manual_seed(5)
+    frames = torch.rand(1024, 3, 12, 20, generator=gen).half().cuda()
+    model = R.load_model(WEIGHTS / artifact, precision=precision)
+    try:
+        out = model.run(frames)
+        for i in (0, 1, 511, 1022, 1023):
+            assert torch.equal(out[i:i + 1], model.run(frames[i:i + 1].contiguous())), f"frame {i}"
     finally:
         model.close()
 
