@@ -157,6 +157,9 @@ def _layer_parity(R, artifact, precision, frames16):
     near = F.pixel_shuffle(_near_tie(t, mag, kind, window).float(), 2) > 0
     counts["expand"] = (int(diff.sum()), int((diff & ~near).sum()), work.numel())
     counts["refine+tail"] = _refine_tail_stage(meta, work, w)
+    top = 448.0 if kind == "e4m3" else 127.0                      # largest code: saturated values
+    say(f"  saturated codes per layer (|code| = {top:g}): {[int((v.abs() == top).sum()) for v in lows]}")
+    counts["saturated"] = sum(int((v.abs() == top).sum()) for v in lows)
     return counts
 
 
@@ -236,16 +239,24 @@ def _report(tag, counts):
     ("div2k mixed 1/f", "aeisu_div2k_l1_mixed_fp8.bin", "mixed", "pink"),
     ("area mixed-fp8mma scene", "aeisu_area_mixed_fp8.bin", "mixed-fp8mma", "scene"),
     ("area fp16 scene", None, "fp16", "scene"),
+    # the scene scaled to [-3, 5]: every E4M3 layer reaches the 448 code and every INT8 layer the 127
+    # clamp, so the saturating requantisation of each layer is compared code for code
+    ("area mixed saturating", "aeisu_area_mixed_fp8.bin", "mixed", "hot"),
+    ("area int8 saturating", None, "int8", "hot"),
 ])
 def test_layer_by_layer_parity(R, tag, artifact, precision, kind):
     from aeisu_amd import frames
     h, wd = 270, 480
     src = frames.pink_noise(h, wd, 3) if kind == "pink" else frames.scene(h, wd, 17, texture=True)
+    if kind == "hot":
+        src = src * 8 - 3
     say(f"case: layer-by-layer parity, {tag}, {h}x{wd}")
     if precision == "fp16":
         counts = _layer_parity_fp16(R, src.half()[None])
     else:
         counts = _layer_parity(R, artifact, precision, src.half()[None])
+        saturated = counts.pop("saturated")
+        assert kind != "hot" or saturated > 0, "the saturating case reached no saturated code"
     _report(tag, counts)
     for stage, (n, bad, total, *far) in counts.items():
         if stage in ("project", "refine+tail") or precision == "fp16":
@@ -255,3 +266,22 @@ def test_layer_by_layer_parity(R, tag, artifact, precision, kind):
         else:
             # the FP8 MFMA rounds inside the unit: code differences in a small fraction
             assert n <= 5e-3 * total, f"{stage}: {n} codes differ"
+
+
+@pytest.mark.parametrize("precision,artifact", [("mixed", "aeisu_area_mixed_fp8.bin"), ("int8", "aeisu_int8_fp16.pt"),
+                                                ("mixed-fp8mma", "aeisu_area_mixed_fp8.bin")])
+def test_fused_equals_per_layer_when_saturating(R, precision, artifact):
+    """The fused body (frame input, 16x16 and 24x24 tiles, with and without the compress exchange)
+    requantises saturated activations exactly as the per-layer path checked above."""
+    from aeisu_amd import _lib as L
+    from aeisu_amd import frames
+    say(f"case: fused == per-layer, {precision}, saturating scene frames 270x480 and 1080x1920")
+    model = R.load_model(WEIGHTS / artifact, precision=precision)
+    try:
+        for h, wd in [(270, 480), (1080, 1920)]:
+            src = (frames.scene(h, wd, 17, texture=True) * 8 - 3).half()[None].cuda().contiguous()
+            per_layer = model.run(src, flags=L.FLAG_UNFUSED)
+            for flags in (0, L.FLAG_BODY_TILE24, L.FLAG_BODY_NO_EXCHANGE):
+                assert torch.equal(model.run(src, flags=flags), per_layer), f"{h}x{wd} flags {flags}"
+    finally:
+        model.close()
