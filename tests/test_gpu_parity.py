@@ -364,6 +364,34 @@ def test_nonfinite_input_raises(fp16_model):
     fp16_model.run(_frame(32, 32, 2)[None].half().cuda().contiguous())   # flag was cleared
 
 
+def test_nonfinite_inputs_raise_in_every_policy(R, fp16_model, mixed_model, int8_model, fp8mma_model):
+    """A NaN or +-Inf anywhere in the frame makes some reconstructed value non-finite in the
+    reference (every input pixel is a tap of some output pixel), so upscale raises
+    FloatingPointError (aeisu/runtime.py:101-102), whatever the policy, the value's position (frame
+    corners included), its frame in the batch, or the launch (eager or graph); the next clean frame
+    passes."""
+    fp32_model = R.load_model(WEIGHTS / "aeisu_area.pt", precision="fp32")
+    try:
+        policies = {"fp16": fp16_model, "mixed": mixed_model, "int8": int8_model, "mixed-fp8mma": fp8mma_model,
+                    "fp32": fp32_model}
+        h, w = 40, 72
+        clean = torch.stack([_frame(h, w, 5), _frame(h, w, 6)]).half().cuda().contiguous()
+        for name, model in policies.items():
+            x0 = clean.float() if name == "fp32" else clean
+            model.run(x0)
+            for value in (float("nan"), float("inf"), float("-inf")):
+                for b, y, xx in [(0, 0, 0), (1, h - 1, w - 1), (1, h // 2, 37)]:
+                    for graph in (False, True):
+                        x = x0.clone()
+                        x[b, (y + xx) % 3, y, xx] = value
+                        say(f"case: {name}, {value} at frame {b} ({y}, {xx}), graph={graph}")
+                        with pytest.raises(FloatingPointError):
+                            model.run(x, graph=graph)
+                model.run(x0)                                            # the flag was cleared
+    finally:
+        fp32_model.close()
+
+
 # ------------------------------------------------------------------------------------------------
 # Mixed FP8 and INT8 policies vs their emulation
 # ------------------------------------------------------------------------------------------------
