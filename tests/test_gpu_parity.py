@@ -487,3 +487,21 @@ def test_mixed_psnr_delta_vs_target(mixed_model):
     say(f"  Y-PSNR gpu {y_psnr(got, hr):.4f} emu {y_psnr(ref, hr):.4f} delta {d:.4f} dB")
     assert abs(d) <= 0.05
     assert (got - ref).abs().max().item() <= 2 / 255
+
+
+@pytest.mark.parametrize("name", ["fp16", "mixed", "int8", "mixed-fp8mma"])
+def test_layouts_agree(fp16_model, mixed_model, int8_model, fp8mma_model, name):
+    """Input and output layouts change storage only: an FP16 frame passed as FP32 gives the same
+    values (the arithmetic is FP32 either way; the FP32-input head tile is laid out differently), and
+    the FP16 output is the FP32 output rounded to nearest even (both clipped to [0, 1] first)."""
+    model = {"fp16": fp16_model, "mixed": mixed_model, "int8": int8_model, "mixed-fp8mma": fp8mma_model}[name]
+    say(f"case: {name}, 1080p, FP16/FP32 input and output layouts")
+    x16 = _frame(1080, 1920, 8)[None].half().cuda().contiguous()
+    x32 = x16.float()
+    o16_16 = model.run(x16, out_dtype=torch.float16)
+    o16_32 = model.run(x16, out_dtype=torch.float32)
+    o32_32 = model.run(x32, out_dtype=torch.float32)
+    o32_16 = model.run(x32, out_dtype=torch.float16)
+    assert torch.equal(o16_16, o16_32.half())
+    assert torch.equal(o32_16, o32_32.half())
+    assert torch.equal(o16_32, o32_32)
