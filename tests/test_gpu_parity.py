@@ -505,3 +505,36 @@ def test_layouts_agree(fp16_model, mixed_model, int8_model, fp8mma_model, name):
     assert torch.equal(o16_16, o16_32.half())
     assert torch.equal(o32_16, o32_32.half())
     assert torch.equal(o16_32, o32_32)
+
+
+def _random_shapes(n: int, seed: int):
+    """n seeded (batch, H, W): sides log-uniform in [1, 1300] x [1, 2100], batches of 1-3 frames."""
+    import math
+    import random
+    rng = random.Random(seed)
+    out = []
+    while len(out) < n:
+        h = int(math.exp(rng.uniform(0, math.log(1300))))
+        w = int(math.exp(rng.uniform(0, math.log(2100))))
+        b = rng.choice([1, 1, 2, 3])
+        if b * h * w <= 3_000_000:
+            out.append((b, h, w))
+    return out
+
+
+def test_random_shapes_fused_equals_per_layer(mixed_model, int8_model, fp16_model, fp8mma_model):
+    """60 seeded shapes (ragged sides from 1 to 2,100 pixels, batches of 1-3, FP16 and FP32 frames):
+    whatever body tiles, head tiles and exchange the shape selects, the default path equals the
+    per-layer path, and (quantized policies) the forced 24x24 tiles, bit for bit."""
+    from aeisu_amd import _lib as L
+    policies = {"mixed": mixed_model, "int8": int8_model, "fp16": fp16_model, "mixed-fp8mma": fp8mma_model}
+    for i, (b, h, w) in enumerate(_random_shapes(60, 2026)):
+        say(f"case: random shape {i}: {b}x3x{h}x{w}")
+        x = torch.rand(b, 3, h, w, generator=torch.Generator().manual_seed(i)).half().cuda()
+        for name, model in policies.items():
+            for dt in (torch.float16, torch.float32):
+                xi = x.to(dt).contiguous()
+                fused = model.run(xi)
+                assert torch.equal(fused, model.run(xi, flags=L.FLAG_UNFUSED)), f"{name} {dt} per-layer"
+                if name != "fp16":
+                    assert torch.equal(fused, model.run(xi, flags=L.FLAG_BODY_TILE24)), f"{name} {dt} tile24"
