@@ -538,3 +538,31 @@ def test_random_shapes_fused_equals_per_layer(mixed_model, int8_model, fp16_mode
                 assert torch.equal(fused, model.run(xi, flags=L.FLAG_UNFUSED)), f"{name} {dt} per-layer"
                 if name != "fp16":
                     assert torch.equal(fused, model.run(xi, flags=L.FLAG_BODY_TILE24)), f"{name} {dt} tile24"
+
+
+def test_random_small_shapes_vs_oracles(R, fp16_model, mixed_model, int8_model, area_state):
+    """16 seeded small shapes (at most 120,000 pixels per batch) of scene frames, each policy against
+    its reference with the bounds of the tiny and ragged frames: FP16 and FP32 against the FP32 model
+    (1e-3, 2e-5), Mixed and INT8 against their emulation (2/255)."""
+    fp32_model = R.load_model(WEIGHTS / "aeisu_area.pt", precision="fp32")
+    spyr = D.weights_from_spyr(spyr8f8.read_file(WEIGHTS / "aeisu_area_mixed_fp8.bin"))
+    int8 = D.weights_from_int8(torch.load(WEIGHTS / "aeisu_int8_fp16.pt", map_location="cpu", weights_only=True))
+    f32, f16 = torch.float32, torch.float16
+    shapes = [s for s in _random_shapes(400, 7) if s[0] * s[1] * s[2] <= 120_000][:16]
+    try:
+        for i, (b, h, w) in enumerate(shapes):
+            say(f"case: random small shape {i}: {b}x3x{h}x{w}")
+            src16 = torch.stack([_frame(h, w, 100 + 3 * i + k) for k in range(b)]).half()
+            x = src16.cuda().contiguous()
+            padded = pad_frame(src16.float())
+            fp32 = torch.stack([M.upscale(area_state, s.float(), 0) for s in src16])
+            cases = ((fp16_model, fp32, f32, 1e-3), (fp32_model, fp32, f32, 2e-5),
+                     (mixed_model, crop_output(D.forward(padded, spyr, "mixed", out_dtype=f16), h, w), f16, 2 / 255),
+                     (int8_model, crop_output(D.forward(padded, int8, "int8", out_dtype=f16), h, w), f16, 2 / 255))
+            for model, ref, odt, tol in cases:
+                got = model.run(x, out_dtype=odt).float().cpu()
+                err = (got - ref).abs().max().item()
+                say(f"  {model.precision}: max|gpu - reference| = {err:.3g} (bound {tol:.3g})")
+                assert err <= tol, f"{model.precision} {b}x{h}x{w}"
+    finally:
+        fp32_model.close()
