@@ -411,7 +411,12 @@ struct Runtime {
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
   }
+  // An executable graph may still be running on the caller's stream (aeisu_upscale_graph returns
+  // once it is launched), and HIP does not promise to keep an executable graph's resources (its
+  // kernel-argument memory) alive past hipGraphExecDestroy, so the device is drained first.  This
+  // runs on reconfiguration, on destruction and when the graph cache is full: never per frame.
   void drop_graph() {
+    if (!graphs.empty()) (void)hipDeviceSynchronize();
     for (Graph& gr : graphs) {
       (void)hipGraphExecDestroy(gr.exec);
       (void)hipGraphDestroy(gr.graph);
