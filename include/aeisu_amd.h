@@ -133,7 +133,9 @@ int aeisu_upscale(aeisu_runtime* rt, const void* d_in, void* d_out, void* stream
 
 /* Same as aeisu_upscale_async but replays a HIP graph captured for this
  * (d_in, d_out) pair; recaptured when the pair changes.  Replaces the
- * reference's pre-captured CUDA graph launch (SrcPyrCudaRuntime.cu:4959-5028). */
+ * reference's pre-captured CUDA graph launch (SrcPyrCudaRuntime.cu:4959-5028).
+ * Up to 16 pairs stay captured; the 17th, like aeisu_configure and aeisu_destroy, first waits for
+ * the device to finish its work and then drops the captured graphs. */
 int aeisu_upscale_graph(aeisu_runtime* rt, const void* d_in, void* d_out, void* stream);
 
 /* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP
