@@ -93,3 +93,24 @@ def test_two_runtimes_on_two_streams(R):
     finally:
         a.close()
         b.close()
+
+
+def test_graph_cache_eviction_while_graphs_run(R):
+    """A runtime keeps 16 captured graphs; the 17th (input, output) pair drops them after draining the
+    device, so graphs launched just before, still running, finish on intact resources: 24 pairs
+    launched back to back without a synchronisation all give the eager result."""
+    say("case: Mixed 540x960, 24 graph pairs launched back to back (cache of 16)")
+    model = R.load_model(WEIGHTS / "aeisu_area_mixed_fp8.bin", precision="mixed")
+    try:
+        src = _frames(1, 540, 960, seed=5).cuda().contiguous()
+        want = model.run(src)
+        outs = [torch.empty_like(want) for _ in range(24)]
+        srcs = [src.clone() for _ in range(2)]
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            model.run(srcs[i % 2], out=o, graph=True, check_finite=False)
+        torch.cuda.synchronize()
+        for i, o in enumerate(outs):
+            assert torch.equal(o, want), f"pair {i}"
+    finally:
+        model.close()
