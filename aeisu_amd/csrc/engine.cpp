@@ -407,6 +407,9 @@ struct Runtime {
 
   ~Runtime() {
     if (model) (void)hipSetDevice(model->device);
+    // frames of this runtime may still be running on the caller's stream: their scratch, events and
+    // graphs are released only once the device has finished
+    if (configured || !graphs.empty()) (void)hipDeviceSynchronize();
     drop_graph();
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (capture_stream) (void)hipStreamDestroy(capture_stream);
@@ -1062,6 +1065,7 @@ static void configure(Runtime& rt, int batch, int height, int width, int in_layo
   const ModeWeights& w = rt.model->weights(mode);
   Geometry g = make_geometry(mode, w.project_precise, rt.model->cu_count, batch, height, width, in_layout, out_layout,
                              flags);
+  if (rt.configured) (void)hipDeviceSynchronize();   // earlier frames may still use the scratch freed below
   rt.drop_graph();
   rt.configured = false;
   rt.timed_frames = 0;                 // recorded stage events belong to the previous layout
