@@ -94,3 +94,74 @@ def test_fp32_policy_refuses_the_coefficient_stages(gpu):
     assert out.shape == (1, 3, 80, 112) and bool(torch.isfinite(out).all())
     # the allocation-free entry point's static array (per GPU, held by the process) is reported
     assert f"static_scratch_bytes={72 << 20}" in model.report()
+
+
+def test_sibling_runtimes_on_threads(gpu):
+    """Runtimes are not thread-safe one by one, but siblings sharing one model may run on their own
+    threads (the reference gives each runtime its own engine slot, SrcPyrCudaRuntime.cu:5392-5439):
+    four threads each configure a sibling of one Mixed runtime for its own geometry, switch it to the
+    FP16 policy and back (the FP16 weights are packed and uploaded once, on first use, under the
+    model's lock) and run frames on their own stream, while the other threads do the same; every
+    output equals the single-threaded result and every thread's error message stays its own."""
+    import ctypes
+    import threading
+    from aeisu_amd import _lib as L
+    from aeisu_amd import frames
+    say("case: 4 threads, one sibling runtime each, shared Mixed model, policy switch on first use")
+    lib = L.lib()
+    main = ctypes.c_void_p()
+    blob = (WEIGHTS / "aeisu_area_mixed_fp8.bin").read_bytes()
+    buf = ctypes.create_string_buffer(blob, len(blob))
+    L.check(lib.aeisu_create_from_memory(buf, len(blob), L.PRECISION["mixed"], ctypes.byref(main)))
+    shapes = [(96, 160), (72, 104), (135, 240), (33, 65)]
+    inputs = [frames.scene(h, w, 7 + i, shapes=5, texture=True).half()[None].cuda().contiguous()
+              for i, (h, w) in enumerate(shapes)]
+
+    def run(rt, x, precision, stream):
+        h, w = x.shape[-2:]
+        L.check(lib.aeisu_configure(rt, 1, h, w, L.LAYOUT_F16, L.LAYOUT_F16, L.PRECISION[precision], 0))
+        out = torch.empty(1, 3, 2 * h, 2 * w, dtype=torch.float16, device=x.device)
+        L.check(lib.aeisu_upscale(rt, ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                  ctypes.c_void_p(stream.cuda_stream)))
+        return out
+
+    # single-threaded references on one sibling
+    ref_rt = ctypes.c_void_p()
+    L.check(lib.aeisu_create_sibling(main, ctypes.byref(ref_rt)))
+    s0 = torch.cuda.Stream()
+    want = {(i, p): run(ref_rt, x, p, s0).cpu() for i, x in enumerate(inputs) for p in ("mixed", "fp16")}
+    lib.aeisu_destroy(ref_rt)
+    # a fresh model, so that the FP16 weights are uploaded on first use inside the threads
+    lib.aeisu_destroy(main)
+    L.check(lib.aeisu_create_from_memory(buf, len(blob), L.PRECISION["mixed"], ctypes.byref(main)))
+    errors, results = [], {}
+    barrier = threading.Barrier(len(inputs))
+
+    def worker(i):
+        try:
+            rt = ctypes.c_void_p()
+            L.check(lib.aeisu_create_sibling(main, ctypes.byref(rt)))
+            stream = torch.cuda.Stream()
+            barrier.wait()
+            for rep in range(3):
+                for p in ("mixed", "fp16"):
+                    results[(i, p, rep)] = run(rt, inputs[i], p, stream).cpu()
+            # this thread's own error message, unaffected by the others
+            bad = lib.aeisu_configure(rt, 1, 9000, 16, 0, 0, 0, 0)
+            msg = lib.aeisu_last_error().decode()
+            if bad != L.AEISU_ERR_INVALID_ARGUMENT or "8192" not in msg:
+                errors.append(f"thread {i}: rc {bad} message {msg!r}")
+            lib.aeisu_destroy(rt)
+        except Exception as e:                              # reported below
+            errors.append(f"thread {i}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(inputs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    lib.aeisu_destroy(main)
+    assert not errors, errors
+    assert len(results) == len(inputs) * 2 * 3
+    for (i, p, rep), got in results.items():
+        assert torch.equal(got, want[(i, p)]), f"thread {i} {p} rep {rep}"
