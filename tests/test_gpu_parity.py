@@ -336,13 +336,15 @@ def test_fused_path_intermediates_and_stages(mixed_model, int8_model, fp8mma_mod
             assert model.intermediate(hd, L.BUF_SKIP).numel() > 0
 
 
-def test_batch_and_graph_consistency(fp16_model, mixed_model):
+def test_batch_and_graph_consistency(R, fp16_model, mixed_model, int8_model, fp8mma_model):
     """Batch independence, and graph replays against the eager result with eager frames in between
-    (the Mixed body's compress exchange counts launches, eager and replayed alike)."""
+    (the Mixed body's compress exchange counts launches, eager and replayed alike), in every policy
+    (the FP32 policy's per-layer kernels included)."""
     say("case: batch-2 vs per-frame, graph vs eager")
     a, b = _frame(64, 64, 21), _frame(64, 64, 22)
     x = torch.stack((a, b)).half().cuda().contiguous()
-    for model in (fp16_model, mixed_model):
+    fp32_model = R.load_model(WEIGHTS / "aeisu_area.pt", precision="fp32")
+    for model in (fp16_model, mixed_model, int8_model, fp8mma_model, fp32_model):
         both = model.run(x)
         one = model.run(x[:1].contiguous())
         two = model.run(x[1:].contiguous())
@@ -353,6 +355,7 @@ def test_batch_and_graph_consistency(fp16_model, mixed_model):
             torch.cuda.synchronize()
             assert torch.equal(out, both)
             assert torch.equal(model.run(x), both)
+    fp32_model.close()
 
 
 def test_nonfinite_input_raises(fp16_model):
