@@ -1315,6 +1315,27 @@ int aeisu_upscale_graph(aeisu_runtime* h, const void* d_in, void* d_out, void* s
         throw;
       }
       aeisu::check_hip(hipStreamEndCapture(rt.capture_stream, &graph), "hipStreamEndCapture");
+      // Topology check (as the reference checks its captured graph, SrcPyrCudaRuntime.cu:4914-4941): a
+      // frame is kernel launches only.  A memset or copy node would also be replayed with every frame,
+      // and memset nodes are not trusted to replay correctly here, so none may have been captured.
+      {
+        size_t n = 0;
+        hipError_t ge = hipGraphGetNodes(graph, nullptr, &n);
+        std::vector<hipGraphNode_t> nodes(n);
+        if (ge == hipSuccess && n) ge = hipGraphGetNodes(graph, nodes.data(), &n);
+        size_t kernels = 0;
+        for (size_t i = 0; ge == hipSuccess && i < n; ++i) {
+          hipGraphNodeType type;
+          ge = hipGraphNodeGetType(nodes[i], &type);
+          kernels += ge == hipSuccess && type == hipGraphNodeTypeKernel;
+        }
+        if (ge != hipSuccess || n == 0 || kernels != n) {
+          (void)hipGraphDestroy(graph);
+          aeisu::fail(AEISU_ERR_HIP, ge != hipSuccess ? std::string("reading the captured frame graph: ") + hipGetErrorString(ge)
+                                                      : "captured frame graph holds " + std::to_string(n - kernels) +
+                                                            " non-kernel node(s) among " + std::to_string(n));
+        }
+      }
       const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
       if (e != hipSuccess) {
         (void)hipGraphDestroy(graph);
