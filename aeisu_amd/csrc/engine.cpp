@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <functional>
@@ -36,6 +37,26 @@ struct Error : std::runtime_error {
 [[noreturn]] static void fail(int code, const std::string& msg) { throw Error(code, msg); }
 static void check_hip(hipError_t e, const char* what) {
   if (e != hipSuccess) fail(AEISU_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Diagnostic, off by default (the reference's AESS_NEURAL_EAGER_VALIDATE, SrcPyrCudaRuntime.cu:5349-5354):
+// with AEISU_EAGER_VALIDATE=1 in the environment every kernel launch outside graph capture is followed
+// by a synchronisation of its stream, so that an asynchronous failure is reported with the launch
+// that caused it instead of at a later call.
+static bool eager_validate() {
+  static const bool on = [] {
+    const char* v = std::getenv("AEISU_EAGER_VALIDATE");
+    return v && v[0] == '1';
+  }();
+  return on;
+}
+static void check_launch(hipError_t e, const char* what, hipStream_t s) {
+  check_hip(e, what);
+  if (!eager_validate()) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  check_hip(hipStreamIsCapturing(s, &cs), what);
+  if (cs != hipStreamCaptureStatusNone) return;
+  check_hip(hipStreamSynchronize(s), what);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -909,8 +930,8 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
         Q.work = P.work + size_t(f0) * g.Hq * g.Wq * 32;
         Q.xbuf = static_cast<unsigned char*>(sc.xbuf) + size_t(f0) * g.Hl * g.Wl * 64;
         Q.xflags = sc.xflags + size_t(f0) * per_frame;
-        check_hip(launch_body_fused_xc(m, src, Q, std::min(g.body_xc_frames, g.batch - f0), g.body_xc_tile, g.cus, s),
-                  "fused body launch");
+        check_launch(launch_body_fused_xc(m, src, Q, std::min(g.body_xc_frames, g.batch - f0), g.body_xc_tile, g.cus, s),
+                     "fused body launch", s);
       }
     } else if (g.body_cols24 > 0) {                       // right-hand columns on 16x16 tiles
       BodyFusedArgs Q = P;
@@ -918,21 +939,21 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
       P.cols = g.body_cols24;
       Q.col0 = g.body_cols24;
       Q.cols = g.Wl - g.body_cols24;
-      check_hip(launch_body_fused_pair(m, src, P, g.batch, 24, Q, g.batch, 16, s), "fused body launch");
+      check_launch(launch_body_fused_pair(m, src, P, g.batch, 24, Q, g.batch, 16, s), "fused body launch", s);
     } else if (k == g.batch) {
-      check_hip(launch_body_fused(m, src, P, k, 24, s), "fused body launch");
+      check_launch(launch_body_fused(m, src, P, k, 24, s), "fused body launch", s);
     } else {                                       // trailing frames on 16x16 tiles
       BodyFusedArgs Q = P;
       Q.frames = static_cast<const char*>(P.frames) + size_t(k) * 3 * g.H * g.W * (g.in_fp32 ? 4 : 2);
       Q.work = P.work + size_t(k) * g.Hq * g.Wq * 32;
-      if (k == 0) check_hip(launch_body_fused(m, src, Q, g.batch, 16, s), "fused body launch");
-      else check_hip(launch_body_fused_pair(m, src, P, k, 24, Q, g.batch - k, 16, s), "fused body launch");
+      if (k == 0) check_launch(launch_body_fused(m, src, Q, g.batch, 16, s), "fused body launch", s);
+      else check_launch(launch_body_fused_pair(m, src, P, k, 24, Q, g.batch - k, 16, s), "fused body launch", s);
     }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }
-  check_hip(launch_project(g.in_fp32, w.project_precise, d_in, w.project.frag.ptr, w.project.bias.as<float>(), sc.skip,
-                           w.analysis, g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, g.grid.project, s), "project launch");
+  check_launch(launch_project(g.in_fp32, w.project_precise, d_in, w.project.frag.ptr, w.project.bias.as<float>(), sc.skip,
+                              w.analysis, g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, g.grid.project, s), "project launch", s);
   if (ev) check_hip(hipEventRecord(ev[1], s), "hipEventRecord");
   const float* A = w.act;
   if (g.fused) {
@@ -952,51 +973,51 @@ static void enqueue_body(const ModeWeights& w, const Geometry& g, const Scratch&
     P.Hl = g.Hl;
     P.Wl = g.Wl;
     if (m != 0 || g.body_rows16 >= g.Hl) {
-      check_hip(launch_body_fused(m, BodySrc::Skip, P, g.batch, 0, s), "fused body launch");
+      check_launch(launch_body_fused(m, BodySrc::Skip, P, g.batch, 0, s), "fused body launch", s);
     } else {                                       // FP16 policy: bottom rows on 8x8 tiles
       BodyFusedArgs Q = P;
       Q.row0 = g.body_rows16;
       Q.rows = g.Hl - g.body_rows16;
       if (g.body_rows16 == 0) {
-        check_hip(launch_body_fused(m, BodySrc::Skip, Q, g.batch, 8, s), "fused body launch");
+        check_launch(launch_body_fused(m, BodySrc::Skip, Q, g.batch, 8, s), "fused body launch", s);
       } else {
         P.row0 = 0;
         P.rows = g.body_rows16;
-        check_hip(launch_body_fused_pair(m, BodySrc::Skip, P, g.batch, 16, Q, g.batch, 8, s), "fused body launch");
+        check_launch(launch_body_fused_pair(m, BodySrc::Skip, P, g.batch, 16, Q, g.batch, 8, s), "fused body launch", s);
       }
     }
     if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
     return;
   }
-  check_hip(launch_compress(m, sc.skip, w.compress.frag.ptr, w.compress.bias.as<float>(), w.compress.scale.as<float>(),
-                            sc.low[low_slot(g, 0)], m ? inv(A[1]) : 0.f, m ? inv(A[2]) : 0.f, g.Hl, g.Wl, g.batch,
-                            g.grid.compress, s), "compress launch");
+  check_launch(launch_compress(m, sc.skip, w.compress.frag.ptr, w.compress.bias.as<float>(), w.compress.scale.as<float>(),
+                               sc.low[low_slot(g, 0)], m ? inv(A[1]) : 0.f, m ? inv(A[2]) : 0.f, g.Hl, g.Wl, g.batch,
+                               g.grid.compress, s), "compress launch", s);
   if (ev) check_hip(hipEventRecord(ev[2], s), "hipEventRecord");
   for (int i = 0; i < 4; ++i) {
-    check_hip(launch_grouped(m, sc.low[low_slot(g, i)], w.grouped[i].frag.ptr, w.grouped[i].bias.as<float>(),
-                             w.grouped[i].scale.as<float>(), sc.low[low_slot(g, i + 1)], m ? inv(A[i + 3]) : 0.f,
-                             g.Hl, g.Wl, g.batch, g.grid.grouped, s), "bottleneck launch");
+    check_launch(launch_grouped(m, sc.low[low_slot(g, i)], w.grouped[i].frag.ptr, w.grouped[i].bias.as<float>(),
+                                w.grouped[i].scale.as<float>(), sc.low[low_slot(g, i + 1)], m ? inv(A[i + 3]) : 0.f,
+                                g.Hl, g.Wl, g.batch, g.grid.grouped, s), "bottleneck launch", s);
   }
   if (ev) check_hip(hipEventRecord(ev[3], s), "hipEventRecord");
-  check_hip(launch_expand(m, sc.low[low_slot(g, 4)], sc.skip, w.expand.frag.ptr, w.expand.bias.as<float>(),
-                          w.expand.scale.as<float>(), sc.work, m ? inv(A[7]) : 0.f, m ? A[7] : 0.f, g.Hl, g.Wl,
-                          g.batch, g.grid.expand, s), "expand launch");
+  check_launch(launch_expand(m, sc.low[low_slot(g, 4)], sc.skip, w.expand.frag.ptr, w.expand.bias.as<float>(),
+                             w.expand.scale.as<float>(), sc.work, m ? inv(A[7]) : 0.f, m ? A[7] : 0.f, g.Hl, g.Wl,
+                             g.batch, g.grid.expand, s), "expand launch", s);
   if (ev) check_hip(hipEventRecord(ev[4], s), "hipEventRecord");
 }
 
 static void enqueue_controller(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in,
                                void* d_meta, hipStream_t s, hipEvent_t* ev) {
   enqueue_body(w, g, sc, d_in, s, ev);
-  check_hip(launch_refine_tail(sc.work, w.refine_tail.frag.ptr, w.refine_tail.bias.as<float>(),
-                               w.tail_bias.as<float>(), d_meta, g.Hq, g.Wq, g.batch, g.grid.refine, s),
-            "refine/tail launch");
+  check_launch(launch_refine_tail(sc.work, w.refine_tail.frag.ptr, w.refine_tail.bias.as<float>(),
+                                  w.tail_bias.as<float>(), d_meta, g.Hq, g.Wq, g.batch, g.grid.refine, s),
+               "refine/tail launch", s);
   if (ev) check_hip(hipEventRecord(ev[5], s), "hipEventRecord");
 }
 
 static void enqueue_head(const ModeWeights& w, const Geometry& g, const Scratch& sc, const void* d_in,
                          const void* d_meta, void* d_out, hipStream_t s) {
-  check_hip(launch_head(g.in_fp32, g.out_fp32, g.qclamp, d_in, d_meta, w.head.frag.ptr, d_out, g.H, g.W, g.Hq, g.Wq,
-                        g.py, g.px, g.batch, sc.nonfinite, g.grid.head, s), "head launch");
+  check_launch(launch_head(g.in_fp32, g.out_fp32, g.qclamp, d_in, d_meta, w.head.frag.ptr, d_out, g.H, g.W, g.Hq, g.Wq,
+                           g.py, g.px, g.batch, sc.nonfinite, g.grid.head, s), "head launch", s);
 }
 
 // FP32 policy: project, compress, 4 grouped, expand, refine + tail, head; events 0..6 as the per-layer path
@@ -1005,13 +1026,13 @@ static void enqueue_fp32(const ModeWeights& w, const Geometry& g, const Scratch&
   if (ev) check_hip(hipEventRecord(ev[0], s), "hipEventRecord");
   float* lows[5];
   for (int i = 0; i < 5; ++i) lows[i] = static_cast<float*>(sc.low[i]);
-  check_hip(launch_f32_controller(g.in_fp32, d_in, w.fp32.as<float>(), static_cast<float*>(sc.skip), lows[0], lows[1],
-                                  g.nlow == 5 ? lows : nullptr, static_cast<float*>(sc.work), static_cast<float*>(sc.meta),
-                                  g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, s, ev),
-            "FP32 controller launch");
-  check_hip(launch_f32_head(g.in_fp32, g.out_fp32, d_in, static_cast<const float*>(sc.meta), w.fp32.as<float>(), d_out,
-                            g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, s),
-            "FP32 head launch");
+  check_launch(launch_f32_controller(g.in_fp32, d_in, w.fp32.as<float>(), static_cast<float*>(sc.skip), lows[0], lows[1],
+                                     g.nlow == 5 ? lows : nullptr, static_cast<float*>(sc.work), static_cast<float*>(sc.meta),
+                                     g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, s, ev),
+               "FP32 controller launch", s);
+  check_launch(launch_f32_head(g.in_fp32, g.out_fp32, d_in, static_cast<const float*>(sc.meta), w.fp32.as<float>(), d_out,
+                               g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, s),
+               "FP32 head launch", s);
   if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
 }
 
@@ -1029,10 +1050,10 @@ static void enqueue_frame(const ModeWeights& w, const Geometry& g, const Scratch
   }
   // fused path: events 0, (1,) 3, 6 only; the head stage times refine + tail + head (3 -> 6)
   enqueue_body(w, g, sc, d_in, s, ev);
-  check_hip(launch_fused_tail_head(g.in_fp32, g.out_fp32, g.qclamp, sc.work, d_in, w.refine_tail.frag.ptr,
-                                   w.refine_tail.bias.as<float>(), w.tail_bias.as<float>(), w.head.frag.ptr, d_out,
-                                   g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, g.grid.fused, s),
-            "fused refine/tail/head launch");
+  check_launch(launch_fused_tail_head(g.in_fp32, g.out_fp32, g.qclamp, sc.work, d_in, w.refine_tail.frag.ptr,
+                                      w.refine_tail.bias.as<float>(), w.tail_bias.as<float>(), w.head.frag.ptr, d_out,
+                                      g.H, g.W, g.Hq, g.Wq, g.py, g.px, g.batch, sc.nonfinite, g.grid.fused, s),
+               "fused refine/tail/head launch", s);
   if (ev) check_hip(hipEventRecord(ev[6], s), "hipEventRecord");
 }
 

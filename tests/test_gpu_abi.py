@@ -165,3 +165,43 @@ def test_sibling_runtimes_on_threads(gpu):
     assert len(results) == len(inputs) * 2 * 3
     for (i, p, rep), got in results.items():
         assert torch.equal(got, want[(i, p)]), f"thread {i} {p} rep {rep}"
+
+
+_EAGER_CHILD = """
+import sys, torch
+from aeisu_amd import runtime as R
+from aeisu_amd import _lib as L
+out = {}
+x = (torch.rand(2, 3, 135, 240, generator=torch.Generator().manual_seed(3)) * 0.9 + 0.05).half().cuda()
+for name, path in [("mixed", "aeisu_area_mixed_fp8.bin"), ("int8", "aeisu_int8_fp16.pt"), ("fp16", "aeisu_area.pt"),
+                   ("fp32", "aeisu_area.pt")]:
+    m = R.load_model("weights/" + path, precision=name)
+    out[name] = m.run(x).cpu()
+    out[name + "_graph"] = m.run(x, graph=True).cpu()
+    out[name + "_unfused"] = m.run(x, flags=L.FLAG_UNFUSED).cpu()
+    m.close()
+torch.save(out, sys.argv[1])
+"""
+
+
+def test_eager_validation_mode(gpu, tmp_path):
+    """AEISU_EAGER_VALIDATE=1 (the reference's AESS_NEURAL_EAGER_VALIDATE diagnostic,
+    SrcPyrCudaRuntime.cu:5349-5354) synchronises the stream after every launch outside graph capture;
+    a process run with it gives the same frames, eager, graph and per-layer, in every policy."""
+    import os
+    from aeisu_amd import runtime as R
+    say("case: a child process with AEISU_EAGER_VALIDATE=1, every policy, eager / graph / per-layer")
+    script = tmp_path / "eager_child.py"
+    script.write_text(_EAGER_CHILD)
+    result = tmp_path / "frames.pt"
+    env = dict(os.environ, AEISU_EAGER_VALIDATE="1", PYTHONPATH=str(ROOT))
+    subprocess.run([sys.executable, str(script), str(result)], cwd=str(ROOT), env=env, check=True, timeout=240)
+    got = torch.load(result, weights_only=True)
+    x = (torch.rand(2, 3, 135, 240, generator=torch.Generator().manual_seed(3)) * 0.9 + 0.05).half().cuda()
+    for name, path in [("mixed", "aeisu_area_mixed_fp8.bin"), ("int8", "aeisu_int8_fp16.pt"),
+                       ("fp16", "aeisu_area.pt"), ("fp32", "aeisu_area.pt")]:
+        m = R.load_model(WEIGHTS / path, precision=name)
+        want = m.run(x).cpu()
+        m.close()
+        for kind in ("", "_graph", "_unfused"):
+            assert torch.equal(got[name + kind], want), name + kind
