@@ -15,8 +15,9 @@
 // gfx950 mapping: a block computes an 8x32 packed tile.  The RGB of the tile's
 // 18x66 LR halo region is staged in LDS with coalesced row loads (one global read
 // per source pixel per tile; the next tile's RGB is loaded into registers while the
-// current one is computed).  Each thread computes the luma of the 4x4 LR window
-// around its packed pixel and the pixel's 32 features into an LDS row; each wave then
+// current one is computed), together with each region pixel's luma, computed once at the
+// store.  Each thread reads the luma of the 4x4 LR window around its packed pixel and the
+// RGB of its 2x2 pixels and writes the pixel's 32 features into an LDS row; each wave then
 // runs MFMAs (16x16x32 f16) per 16 of its own pixels against register-resident
 // project weights.  Two workgroup barriers per tile.
 //
@@ -35,26 +36,27 @@ namespace aeisu {
 constexpr int kPTW = 32, kPTH = 8;
 constexpr int kPLW = 2 * kPTW + 2, kPLH = 2 * kPTH + 2;
 // halves per LDS feature row: 32 features + 8 pad.  The FP32-accurate variant passes its high and
-// low parts through the same rows one after the other, so that the block's LDS (34.8 KB) lets four
-// blocks share a CU instead of three.
+// low parts through the same rows one after the other, so that the block's LDS (39.5 KB with the
+// luma plane) lets four blocks share a CU instead of three.
 constexpr int kPFeat = 40;
 
 constexpr int kPRgb = kPLH * kPLW;                       // LR pixels of the halo region
-constexpr int kPRows = 3 * kPLH;                         // region rows of the three channels (54)
-constexpr int kPRowIters = (kPRows + 3) / 4;             // rows per wave (four waves)
-constexpr int kPExtra = kPRows * (kPLW - 64);            // values in columns 64..65 (108)
-static_assert(kPLW >= 64 && kPLW - 64 <= 2 && kPExtra <= 256, "one extra column value per thread");
+constexpr int kPRowIters = (kPLH + 3) / 4;               // region rows per wave (four waves)
+constexpr int kPExtra = kPLH * (kPLW - 64);              // pixels in columns 64..65 (36)
+static_assert(kPLW >= 64 && kPLW - 64 <= 2 && kPExtra <= 256, "one extra column pixel per thread");
 
 // The halo RGB of the next tile is held as raw frame values and converted when stored to
 // LDS (converting at load time would make the compiler wait for every load on the spot).
-// Region rows are taken row-wise: wave w loads rows w, w + 4, ... of the 54 channel rows,
-// lane l column l, so a load is one buffer instruction with the lane's column offset (computed
-// once per tile) and a wave-uniform row offset; columns 64 and 65 of the 54 rows are one value
-// each for threads 0..107.  Coordinates are clamped to the source (replicate padding).
+// Region rows are taken row-wise: wave w loads the three channels of rows w, w + 4, ... of the
+// 18 region rows, lane l column l, so a load is one buffer instruction with the lane's column
+// offset (computed once per tile) and a wave-uniform row offset; the pixels of columns 64 and 65
+// are one each for threads 0..35.  Each thread so holds whole pixels and stores each pixel's luma
+// beside its RGB, once per LR pixel instead of once per 4x4 window that contains it.  Coordinates
+// are clamped to the source (replicate padding).
 template <typename Tin>
 struct ProjectStage {
-  Tin v[kPRowIters];
-  Tin x;
+  Tin v[kPRowIters][3];
+  Tin x[3];
 };
 template <typename Tin>
 __device__ __forceinline__ void project_fetch(ProjectStage<Tin>& st, const Tin* __restrict__ src, int b, int Y0,
@@ -66,33 +68,52 @@ __device__ __forceinline__ void project_fetch(ProjectStage<Tin>& st, const Tin* 
   const int vx = min(max(X0 + l - px, 0), W - 1) * (int)sizeof(Tin);
 #pragma unroll
   for (int i = 0; i < kPRowIters; ++i) {
-    const int R = min(w + 4 * i, kPRows - 1);            // wave-uniform
-    const int c = R / kPLH, r = R - c * kPLH;
+    const int r = min(w + 4 * i, kPLH - 1);              // wave-uniform
     const int sy = min(max(Y0 + r - py, 0), H - 1);
-    const int so = c * plane + sy * W * (int)sizeof(Tin);
-    if constexpr (sizeof(Tin) == 2) st.v[i] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, vx, so, 0));
-    else st.v[i] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, vx, so, 0));
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const int so = c * plane + sy * W * (int)sizeof(Tin);
+      if constexpr (sizeof(Tin) == 2) st.v[i][c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, vx, so, 0));
+      else st.v[i][c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, vx, so, 0));
+    }
   }
   {
     const int q = min(tid, kPExtra - 1);
-    const int R = q >> 1, col = 64 + (q & 1);
-    const int c = R / kPLH, r = R - c * kPLH;
+    const int r = q >> 1, col = 64 + (q & 1);
     const int sy = min(max(Y0 + r - py, 0), H - 1), sx = min(max(X0 + col - px, 0), W - 1);
     const int o = (sy * W + sx) * (int)sizeof(Tin);
-    if constexpr (sizeof(Tin) == 2) st.x = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, o, c * plane, 0));
-    else st.x = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, o, c * plane, 0));
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      if constexpr (sizeof(Tin) == 2) st.x[c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b16(rs, o, c * plane, 0));
+      else st.x[c] = __builtin_bit_cast(Tin, __builtin_amdgcn_raw_buffer_load_b32(rs, o, c * plane, 0));
+    }
   }
 }
-// Stage -> LDS (planar FP32 [c][r][col]); rows past the 54th were loaded clamped and are not stored.
+// Stage -> LDS: planar FP32 RGB [c][r][col] and the luma [r][col] of every region pixel; rows past
+// the 18th were loaded clamped and are not stored.
 template <typename Tin>
-__device__ __forceinline__ void project_store(const ProjectStage<Tin>& st, float* rgb, int tid) {
+__device__ __forceinline__ void project_store(const ProjectStage<Tin>& st, float* rgb, float* lum, const Analysis& an,
+                                              int tid) {
   const int w = tid >> 6, l = tid & 63;
 #pragma unroll
   for (int i = 0; i < kPRowIters; ++i) {
-    const int R = w + 4 * i;
-    if (R < kPRows) rgb[R * kPLW + l] = (float)st.v[i];
+    const int r = w + 4 * i;
+    if (r < kPLH) {
+      const float v0 = (float)st.v[i][0], v1 = (float)st.v[i][1], v2 = (float)st.v[i][2];
+      rgb[r * kPLW + l] = v0;
+      rgb[kPRgb + r * kPLW + l] = v1;
+      rgb[2 * kPRgb + r * kPLW + l] = v2;
+      lum[r * kPLW + l] = luma(v0, v1, v2, an);
+    }
   }
-  if (tid < kPExtra) rgb[(tid >> 1) * kPLW + 64 + (tid & 1)] = (float)st.x;
+  if (tid < kPExtra) {
+    const int o = (tid >> 1) * kPLW + 64 + (tid & 1);
+    const float v0 = (float)st.x[0], v1 = (float)st.x[1], v2 = (float)st.x[2];
+    rgb[o] = v0;
+    rgb[kPRgb + o] = v1;
+    rgb[2 * kPRgb + o] = v2;
+    lum[o] = luma(v0, v1, v2, an);
+  }
 }
 
 template <typename Tin, bool PRECISE>
@@ -100,6 +121,7 @@ __global__ __launch_bounds__(256) void project_kernel(
     const Tin* __restrict__ src, const h8* __restrict__ wfrag, const float* __restrict__ bias,
     _Float16* __restrict__ skip, Analysis an, int H, int W, int Hq, int Wq, int py, int px, int batch) {
   __shared__ float rgb[3][kPLH][kPLW];
+  __shared__ float lum[kPLH][kPLW];
   __shared__ __attribute__((aligned(16))) _Float16 feat[kPTH * kPTW][kPFeat];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -139,7 +161,7 @@ __global__ __launch_bounds__(256) void project_kernel(
     int b, qy0, qx0;
     origin(tidx, b, qy0, qx0);
     lds_barrier();                                    // previous tile's RGB reads done
-    project_store<Tin>(st, &rgb[0][0][0], tid);
+    project_store<Tin>(st, &rgb[0][0][0], &lum[0][0], an, tid);
     {
       const int tn = tile_of(it + 1, num_tiles);      // next tile's RGB in flight during this one
       if (tn < num_tiles) {
@@ -151,8 +173,18 @@ __global__ __launch_bounds__(256) void project_kernel(
     lds_barrier();
     h8 bop[4], blo[4];
     {
-      float f[8][4];
-      packed_features(&rgb[0][2 * ty][2 * tx], kPLH * kPLW, kPLW, an, f);
+      float f[8][4], lw[4][4], cw[3][2][2];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) lw[a][b] = lum[2 * ty + a][2 * tx + b];
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) cw[c][i][j] = rgb[c][2 * ty + 1 + i][2 * tx + 1 + j];
+      luma_features(lw, cw, an, f);
       h8 hi[4], lo[4];
       feature_slices<PRECISE>(f, hi, lo);
 #pragma unroll
